@@ -1,0 +1,286 @@
+"""Per-kernel parity: each HIP kernel (through the C ABI wrappers) against a float64
+CPU restatement of the same op on the same FP16-rounded operands.
+
+Tolerances are stated per test; they bound FP32 accumulation-order differences
+and, where an intermediate is rounded to FP16 inside the kernel, one FP16 ulp
+of that intermediate.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+
+
+def _linear(in_f, out_f, device, seed):
+    torch.manual_seed(seed)
+    lin = nn.Linear(in_f, out_f)
+    with torch.no_grad():
+        lin.bias.uniform_(-0.5, 0.5)
+    return lin.half().to(device)
+
+
+def _norm(width, device, seed):
+    g = torch.Generator().manual_seed(seed)
+    norm = nn.LayerNorm(width)
+    with torch.no_grad():
+        norm.weight.copy_(1.0 + 0.1 * torch.randn(width, generator=g))
+        norm.bias.copy_(0.1 * torch.randn(width, generator=g))
+    return norm.to(device)
+
+
+def _randn(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g) * scale
+
+
+def _ln64(r, norm):
+    w = norm.weight.detach().cpu().double()
+    b = norm.bias.detach().cpu().double()
+    mean = r.mean(-1, keepdim=True)
+    var = ((r - mean) ** 2).mean(-1, keepdim=True)
+    return (r - mean) / torch.sqrt(var + norm.eps) * w + b
+
+
+def _close(actual, expected, atol, rtol, what):
+    actual = actual.detach().cpu().double()
+    expected = expected.double()
+    err = (actual - expected).abs()
+    bound = atol + rtol * expected.abs()
+    bad = int((err > bound).sum())
+    assert torch.isfinite(actual).all(), f"{what}: non-finite output"
+    assert bad == 0, f"{what}: {bad} elements out of tolerance, max_err={float(err.max()):.3g}"
+
+
+# --------------------------------------------------------------------------- LayerNorm
+
+
+@pytest.mark.parametrize("width", [32, 96, 128, 256, 512, 1024])
+@pytest.mark.parametrize("rows", [1, 37, 4099])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+def test_residual_layernorm(hip_device, width, rows, out_dtype):
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import layer_norm, mixed_add_layer_norm
+
+    x = _randn((rows, width), 1, 3.0)
+    u = _randn((rows, width), 2)
+    norm = _norm(width, hip_device, 3)
+    res, out = mixed_add_layer_norm(x.to(hip_device), u.to(hip_device), norm, normalized_dtype=out_dtype)
+    r64 = x.double() + u.double()
+    _close(res, r64, 0.0, 1e-7, "residual")
+    ref = _ln64(r64, norm)
+    tol = 2e-5 if out_dtype == torch.float32 else 2 ** -10
+    _close(out, ref, tol, tol, "normalized")
+    plain = layer_norm(x.to(hip_device), norm, normalized_dtype=out_dtype)
+    _close(plain, _ln64(x.double(), norm), tol, tol, "plain LN")
+
+
+def test_layernorm_rejects_bad_inputs(hip_device):
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_add_layer_norm
+
+    norm = _norm(128, hip_device, 0)
+    x = torch.zeros(4, 128, device=hip_device)
+    with pytest.raises(ValueError):
+        mixed_add_layer_norm(x.half(), x, norm, normalized_dtype=torch.float16)
+    with pytest.raises(ValueError):
+        mixed_add_layer_norm(x.cpu(), x.cpu(), norm, normalized_dtype=torch.float16)
+    with pytest.raises(ValueError):
+        mixed_add_layer_norm(x, x[:, :64].contiguous(), norm, normalized_dtype=torch.float16)
+
+
+# --------------------------------------------------------------------------- projections
+
+
+def _ref_linear(x, lin, gelu):
+    xh = x.detach().cpu().half().double()
+    w = lin.weight.detach().cpu().double()
+    b = lin.bias.detach().cpu().double()
+    y = xh @ w.t() + b
+    if gelu:
+        y = 0.5 * y * (1.0 + torch.erf(y / math.sqrt(2.0)))
+    return y
+
+
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(8192, 384, 128), (1000, 96, 32), (333, 2048, 512), (5, 64, 64), (4096, 128, 128), (130, 768, 256),
+     (257, 40, 24)],
+)
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
+def test_mixed_linear(hip_device, m, n, k, variant):
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear
+
+    lin = _linear(k, n, hip_device, 7)
+    x32 = _randn((m, k), 11)
+    for in_dtype in (torch.float32, torch.float16):
+        for out_dtype in (torch.float32, torch.float16):
+            for gelu in (False, True):
+                x = x32.to(hip_device, in_dtype)
+                y = mixed_linear(x, lin, output_dtype=out_dtype, fuse_gelu=gelu, variant=variant)
+                assert y.dtype == out_dtype and y.shape == (m, n)
+                ref = _ref_linear(x32, lin, gelu)
+                tol = 1e-5 * math.sqrt(k) if out_dtype == torch.float32 else 2 ** -10
+                _close(y, ref, tol, tol, f"linear in={in_dtype} out={out_dtype} gelu={gelu}")
+
+
+def test_mixed_linear_3d_input(hip_device):
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear
+
+    lin = _linear(128, 384, hip_device, 5)
+    x = _randn((3, 17, 128), 6)
+    y = mixed_linear(x.to(hip_device), lin, output_dtype=torch.float16)
+    assert y.shape == (3, 17, 384)
+    _close(y.reshape(-1, 384), _ref_linear(x.reshape(-1, 128), lin, False), 2 ** -10, 2 ** -10, "3d")
+
+
+@pytest.mark.parametrize("d", [32, 64, 128, 256, 512])
+@pytest.mark.parametrize("m", [7, 1000, 8192])
+@pytest.mark.parametrize("variant", [1, 2])
+def test_linear_residual_layernorm(hip_device, d, m, variant):
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear_add_layer_norm
+
+    lin = _linear(d, d, hip_device, 21)
+    norm = _norm(d, hip_device, 22)
+    x = _randn((m, d), 23)
+    resid = _randn((m, d), 24, 2.0)
+    for in_dtype in (torch.float16, torch.float32):
+        for out_dtype in (torch.float16, torch.float32):
+            r_out, n_out = mixed_linear_add_layer_norm(
+                x.to(hip_device, in_dtype), lin, resid.to(hip_device), norm, normalized_dtype=out_dtype,
+                variant=variant,
+            )
+            r64 = _ref_linear(x, lin, False) + resid.double()
+            _close(r_out, r64, 2e-5 * math.sqrt(d), 1e-6, "residual_out")
+            tol = 5e-5 if out_dtype == torch.float32 else 2 ** -10
+            _close(n_out, _ln64(r64, norm), tol, tol, "normalized_out")
+
+
+@pytest.mark.parametrize("d,f", [(128, 128), (32, 64), (64, 96), (256, 1024), (512, 2048), (128, 512)])
+@pytest.mark.parametrize("m", [9, 3000])
+@pytest.mark.parametrize("variant", [1, 2])
+def test_ffn_residual_layernorm(hip_device, d, f, m, variant):
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_ffn_add_layer_norm
+
+    lin_in = _linear(d, f, hip_device, 31)
+    lin_out = _linear(f, d, hip_device, 32)
+    norm = _norm(d, hip_device, 33)
+    x = _randn((m, d), 34)
+    resid = _randn((m, d), 35, 2.0)
+    for out_dtype in (torch.float16, torch.float32):
+        r_out, n_out = mixed_ffn_add_layer_norm(
+            x.to(hip_device, torch.float16), lin_in, lin_out, resid.to(hip_device), norm,
+            normalized_dtype=out_dtype, variant=variant,
+        )
+        h = _ref_linear(x, lin_in, True)          # FP32 GELU on the accumulator ...
+        h16 = h.float().half()                    # ... rounded to FP16 for the second product
+        w = lin_out.weight.detach().cpu().double()
+        b = lin_out.bias.detach().cpu().double()
+        r64 = h16.double() @ w.t() + b + resid.double()
+        # one FP16 ulp of any hidden value may flip against the float64 reference
+        atol = 2 ** -11 * float(h.abs().max()) * float(w.abs().max()) * 4 + 2e-5 * math.sqrt(f)
+        _close(r_out, r64, atol, 1e-5, "ffn residual_out")
+        tol = max(atol * 10, 1e-4) if out_dtype == torch.float32 else 2 ** -9
+        _close(n_out, _ln64(r64, norm), tol, tol, "ffn normalized_out")
+
+
+def test_fused_ops_reject_unsupported(hip_device):
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_ffn_add_layer_norm, mixed_linear_add_layer_norm
+
+    lin = _linear(96, 96, hip_device, 1)
+    norm = _norm(96, hip_device, 1)
+    x = torch.zeros(4, 96, device=hip_device, dtype=torch.float16)
+    r = torch.zeros(4, 96, device=hip_device)
+    with pytest.raises(ValueError):
+        mixed_linear_add_layer_norm(x, lin, r, norm)
+    with pytest.raises(ValueError):
+        mixed_ffn_add_layer_norm(x, lin, lin, r, norm)
+
+
+# --------------------------------------------------------------------------- attention
+
+
+def _ref_attention(q, k, v, scale, causal, key_valid=None):
+    q = q.detach().cpu().half().double()
+    k = k.detach().cpu().half().double()
+    v = v.detach().cpu().half().double()
+    s = (q @ k.transpose(-1, -2)) * scale
+    S = q.shape[-2]
+    if causal:
+        s = s.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+    if key_valid is not None:
+        s = s.masked_fill(~key_valid.cpu()[:, None, None, :], float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    return (p @ v).permute(0, 2, 1, 3)  # [B, S, H, hd]
+
+
+def _packed_qkv(b, s, h, hd, seed, device, dtype):
+    qkv = _randn((b, s, 3, h, hd), seed, 1.5).to(device, dtype)
+    q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+    return qkv, q, k, v
+
+
+@pytest.mark.parametrize(
+    "b,h,s,hd",
+    [(2, 4, 128, 32), (2, 2, 256, 16), (1, 8, 300, 64), (1, 2, 77, 128), (3, 4, 1024, 32), (1, 1, 1, 32),
+     (2, 3, 65, 16), (1, 2, 2048, 64)],
+)
+@pytest.mark.parametrize("variant", [1, 2])
+def test_fp16_causal_attention(hip_device, b, h, s, hd, variant):
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention, fp16_causal_attention, is_fp16_supported
+
+    _, q, k, v = _packed_qkv(b, s, h, hd, 41, hip_device, torch.float16)
+    scale = hd ** -0.5
+    assert is_fp16_supported(q, k, v, True)
+    out = attention(q, k, v, scale, causal=True, variant=variant)
+    assert out.shape == (b, s, h, hd) and out.dtype == torch.float16 and out.is_contiguous()
+    ref = _ref_attention(q, k, v, scale, True)
+    # P is rounded to FP16 for the P.V product and the output is stored as FP16
+    _close(out, ref, 3e-3, 3e-3, "fp16 causal attention")
+    if variant == 1:
+        _close(fp16_causal_attention(q, k, v, scale), ref, 3e-3, 3e-3, "fp16_causal_attention")
+
+
+@pytest.mark.parametrize("b,h,s,hd", [(2, 4, 128, 32), (1, 2, 200, 64), (2, 2, 96, 16)])
+def test_attention_noncausal_fp32io_and_keymask(hip_device, b, h, s, hd):
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention, causal_attention
+
+    _, q, k, v = _packed_qkv(b, s, h, hd, 43, hip_device, torch.float32)
+    scale = hd ** -0.5
+    out = attention(q, k, v, scale, causal=False)
+    assert out.dtype == torch.float32
+    _close(out, _ref_attention(q, k, v, scale, False), 3e-3, 3e-3, "non-causal fp32 io")
+    _close(causal_attention(q, k, v, scale), _ref_attention(q, k, v, scale, True), 3e-3, 3e-3, "causal fp32 io")
+    lengths = torch.tensor([max(1, s - 17 * (i + 1)) for i in range(b)])
+    key_valid = (torch.arange(s)[None, :] < lengths[:, None]).to(hip_device)
+    out_m = attention(q.half(), k.half(), v.half(), scale, causal=True, key_valid=key_valid)
+    ref_m = _ref_attention(q, k, v, scale, True, key_valid)
+    _close(out_m, ref_m, 3e-3, 3e-3, "causal + key mask")
+
+
+def test_attention_causality_exact(hip_device):
+    """Output row t is bit-identical when keys/values after t change."""
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention
+
+    qkv, q, k, v = _packed_qkv(2, 512, 4, 32, 45, hip_device, torch.float16)
+    base = attention(q, k, v, 32 ** -0.5)
+    t = 300
+    qkv2 = qkv.clone()
+    qkv2[:, t + 1:] = _randn(tuple(qkv2[:, t + 1:].shape), 46).to(hip_device, torch.float16)
+    q2, k2, v2 = qkv2.permute(2, 0, 3, 1, 4).unbind(0)
+    moved = attention(q2, k2, v2, 32 ** -0.5)
+    assert torch.equal(base[:, : t + 1], moved[:, : t + 1])
+    assert not torch.equal(base[:, t + 1:], moved[:, t + 1:])
+
+
+def test_attention_rejects_unsupported(hip_device):
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention, is_fp16_supported
+
+    x = torch.zeros(1, 2, 16, 24, device=hip_device, dtype=torch.float16)
+    assert not is_fp16_supported(x, x, x, True)
+    with pytest.raises(ValueError):
+        attention(x, x, x, 1.0)

@@ -1,0 +1,357 @@
+// Causal flash attention for gfx950: FP16 MFMA for Q K^T and P V, FP32 online
+// softmax statistics and FP32 output accumulation, causal tile skipping.
+//
+// Replaces the reference's Triton kernels
+//   _causal_attention_fp16_fwd  custom_kernel/triton_attention.py:126-232  (FP16 I/O)
+//   _causal_attention_fwd       custom_kernel/triton_attention.py:16-123   (FP32 I/O)
+// Math per query row (same rounding points as the FP16 reference kernel):
+//   s_j = q . k_j  (FP16 operands, FP32 accumulate)
+//   m   = running max of s (FP32);  p_j = 2^(s_j*c - m*c), c = scale*log2(e)
+//   l   = running sum of p_j in FP32;  acc += fp16(p_j) * v_j  (FP32 accumulate)
+//   o   = acc / l, rounded to the output type.
+// For FP32 inputs (the reference's TF32 kernel) q, k, v are rounded to FP16 on
+// load, which keeps the same 10-bit operand mantissa as TF32.
+//
+// Structure.  A workgroup (4 waves) owns QB = 64*QT queries of one (batch, head);
+// each wave owns 16*QT queries.  Key/value tiles of 64 rows are staged through
+// LDS (K row-major, V transposed) with a one-tile register prefetch.  Each wave
+// computes S^T = K Q^T with the paired row mapping (mpk_common.h), so a lane
+// holds one query and 8 consecutive keys per 32-key pair: the row max needs two
+// cross-lane shuffles, and fp16(P) is already laid out as the B operand of
+// O^T = V^T P^T.  Key tiles strictly above a wave's queries are skipped; only
+// tiles that straddle the diagonal (or the sequence end, or carry a key mask)
+// pay for masking.  Workgroups are issued longest-first (last query block first).
+#include "mpk_common.h"
+
+namespace mpk {
+
+constexpr int KT = 64;  // keys per tile
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t qs[4], ks[4], vs[4], os[4];  // element strides: batch, head, seq, dim
+  const uint8_t* key_valid;           // optional [B, S] (row stride S), nonzero = valid key
+  int batch, heads, seq, causal;
+  float c;  // scale * log2(e)
+};
+
+template <int HD>
+struct AttnShape {
+  static constexpr int LDK = HD + 8;   // K tile row stride (halves)
+  static constexpr int LDV = KT + 8;   // V^T tile row stride (halves)
+  static constexpr int CPK = HD / 8;   // 8-element chunks per key row
+  static constexpr int CHUNKS = KT * CPK;
+  static constexpr int PER_THREAD = (CHUNKS + kBlock - 1) / kBlock;
+  static constexpr int DT = HD >= 32 ? HD / 32 : 1;  // output d tiles (pairs of 16, or one tile of 16)
+};
+
+template <int HD, int QT, typename IT, typename OT, bool KEYMASK>
+__global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
+  using SH = AttnShape<HD>;
+  constexpr int QB = 64 * QT;
+  static_assert(HD == 16 || HD == 32 || HD == 64 || HD == 128, "head dim");
+
+  __shared__ _Float16 ks_lds[KT * SH::LDK];
+  __shared__ _Float16 vt_lds[HD * SH::LDV];
+  __shared__ float kbias[KT];
+
+  const int S = a.seq;
+  const int BH = a.batch * a.heads;
+  const int nqb = (S + QB - 1) / QB;
+  const int qblock = nqb - 1 - (int)(blockIdx.x / BH);
+  const int bh = blockIdx.x % BH;
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int q0 = qblock * QB;
+
+  const IT* __restrict__ Q = static_cast<const IT*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const IT* __restrict__ Kp = static_cast<const IT*>(a.k) + b * a.ks[0] + h * a.ks[1];
+  const IT* __restrict__ Vp = static_cast<const IT*>(a.v) + b * a.vs[0] + h * a.vs[1];
+  OT* __restrict__ O = static_cast<OT*>(a.o) + b * a.os[0] + h * a.os[1];
+  const uint8_t* kv_valid = KEYMASK ? a.key_valid + (int64_t)b * S : nullptr;
+
+  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = l & 15, g = l >> 4;
+  const int qw0 = q0 + wave * 16 * QT;       // first query of this wave
+  const int qw_last = qw0 + 16 * QT - 1;     // last query of this wave
+
+  // ---- Q fragments (B operand of S^T = K Q^T), kept in registers ----
+  constexpr int QK_STEPS = HD >= 32 ? HD / 32 : 1;
+  h8 qf[QT][QK_STEPS];
+  h4 qf16[QT];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int q = qw0 + 16 * t + r;
+    if constexpr (HD == 16) {
+      h4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = (_Float16)0.f;
+      if (q < S) {
+        const IT* src = Q + (int64_t)q * a.qs[2] + 4 * g;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (_Float16)src[j];
+      }
+      qf16[t] = v;
+    } else {
+#pragma unroll
+      for (int kq = 0; kq < QK_STEPS; ++kq)
+        qf[t][kq] = q < S ? load8_as_half(Q + (int64_t)q * a.qs[2] + kq * 32 + 8 * g) : zero_h8();
+    }
+  }
+
+  // ---- running statistics and output accumulators ----
+  float m_run[QT], l_run[QT];
+  f4 oacc[QT][SH::DT][2];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    m_run[t] = -INFINITY;
+    l_run[t] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < SH::DT; ++dt) oacc[t][dt][0] = oacc[t][dt][1] = zero4();
+  }
+
+  const int kv_end = a.causal ? min(q0 + QB, S) : S;  // keys [0, kv_end) can matter
+  const int ntiles = (kv_end + KT - 1) / KT;
+
+  // ---- register prefetch of one K/V tile ----
+  h8 kreg[SH::PER_THREAD], vreg[SH::PER_THREAD];
+  float breg = 0.f;
+  auto fetch = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < SH::PER_THREAD; ++i) {
+      const int c = threadIdx.x + i * kBlock;
+      const int key = c / SH::CPK, col = (c % SH::CPK) * 8;
+      const int gk = kb + key;
+      const bool ok = c < SH::CHUNKS && gk < S;
+      kreg[i] = ok ? load8_as_half(Kp + (int64_t)gk * a.ks[2] + col) : zero_h8();
+      vreg[i] = ok ? load8_as_half(Vp + (int64_t)gk * a.vs[2] + col) : zero_h8();
+    }
+    if (threadIdx.x < KT) {
+      const int gk = kb + threadIdx.x;
+      bool valid = gk < S;
+      if (KEYMASK && valid) valid = kv_valid[gk] != 0;
+      breg = valid ? 0.f : -INFINITY;
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < SH::PER_THREAD; ++i) {
+      const int c = threadIdx.x + i * kBlock;
+      if (c < SH::CHUNKS) {
+        const int key = c / SH::CPK, col = (c % SH::CPK) * 8;
+        *reinterpret_cast<h8*>(&ks_lds[key * SH::LDK + col]) = kreg[i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vt_lds[(col + j) * SH::LDV + key] = vreg[i][j];
+      }
+    }
+    if (threadIdx.x < KT) kbias[threadIdx.x] = breg;
+  };
+
+  fetch(0);
+  for (int tile = 0; tile < ntiles; ++tile) {
+    const int kb = tile * KT;
+    __syncthreads();
+    stash();
+    __syncthreads();
+    if (tile + 1 < ntiles) fetch(kb + KT);
+
+    if (a.causal && kb > qw_last) continue;  // whole tile is in this wave's future
+    const bool need_mask = KEYMASK || kb + KT > S || (a.causal && kb + KT - 1 > qw0);
+
+    // ---- S^T = K Q^T for 64 keys x 16*QT queries ----
+    f4 sc[2][2][QT];  // [key pair][tile in pair][q tile]
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int krow = 32 * p + pair_row(r, tt);
+#pragma unroll
+        for (int t = 0; t < QT; ++t) sc[p][tt][t] = zero4();
+        if constexpr (HD == 16) {
+          const h4 ka = *reinterpret_cast<const h4*>(&ks_lds[krow * SH::LDK + 4 * g]);
+#pragma unroll
+          for (int t = 0; t < QT; ++t) sc[p][tt][t] = mfma16(ka, qf16[t], sc[p][tt][t]);
+        } else {
+#pragma unroll
+          for (int kq = 0; kq < QK_STEPS; ++kq) {
+            const h8 ka = *reinterpret_cast<const h8*>(&ks_lds[krow * SH::LDK + kq * 32 + 8 * g]);
+#pragma unroll
+            for (int t = 0; t < QT; ++t) sc[p][tt][t] = mfma32(ka, qf[t][kq], sc[p][tt][t]);
+          }
+        }
+      }
+
+    // ---- online softmax, per query tile ----
+    h8 pf[QT][2];  // fp16(P) as the B operand of the PV product, per key pair
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      const int q = qw0 + 16 * t + r;
+      if (need_mask) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int kl = 32 * p + 8 * g + 4 * tt + i;
+              float s = sc[p][tt][t][i] + kbias[kl];
+              if (a.causal && kb + kl > q) s = -INFINITY;
+              sc[p][tt][t][i] = s;
+            }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[p][tt][t][i]);
+      mx = max_over_groups(mx);
+      const float m_new = fmaxf(m_run[t], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f((m_run[t] - m_use) * a.c);
+      m_run[t] = m_new;
+      const float moff = -m_use * a.c;
+      float psum = 0.f;
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float pv = __builtin_amdgcn_exp2f(fmaf(sc[p][tt][t][i], a.c, moff));
+            psum += pv;
+            pf[t][p][4 * tt + i] = (_Float16)pv;
+          }
+      l_run[t] = l_run[t] * alpha + psum;
+#pragma unroll
+      for (int dt = 0; dt < SH::DT; ++dt) {
+        oacc[t][dt][0] *= alpha;
+        oacc[t][dt][1] *= alpha;
+      }
+    }
+
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if constexpr (HD == 16) {
+        const h8 va = *reinterpret_cast<const h8*>(&vt_lds[r * SH::LDV + 32 * p + 8 * g]);
+#pragma unroll
+        for (int t = 0; t < QT; ++t) oacc[t][0][0] = mfma32(va, pf[t][p], oacc[t][0][0]);
+      } else {
+#pragma unroll
+        for (int dt = 0; dt < SH::DT; ++dt)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            const int drow = 32 * dt + pair_row(r, tt);
+            const h8 va = *reinterpret_cast<const h8*>(&vt_lds[drow * SH::LDV + 32 * p + 8 * g]);
+#pragma unroll
+            for (int t = 0; t < QT; ++t) oacc[t][dt][tt] = mfma32(va, pf[t][p], oacc[t][dt][tt]);
+          }
+      }
+    }
+  }
+
+  // ---- normalise and store ----
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int q = qw0 + 16 * t + r;
+    const float lsum = sum_over_groups(l_run[t]);
+    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    if (q >= S) continue;
+    OT* dst = O + (int64_t)q * a.os[2];
+    if constexpr (HD == 16) {
+      // lane group g holds d = 4g .. 4g+3
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[4 * g + i] = (OT)(oacc[t][0][0][i] * inv);
+    } else {
+#pragma unroll
+      for (int dt = 0; dt < SH::DT; ++dt) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = oacc[t][dt][0][i] * inv;
+          v[4 + i] = oacc[t][dt][1][i] * inv;
+        }
+        store8(dst + 32 * dt + 8 * g, v);
+      }
+    }
+  }
+}
+
+template <int HD, int QT, typename IT, typename OT>
+static hipError_t launch_attn(const AttnArgs& a, hipStream_t s) {
+  constexpr int QB = 64 * QT;
+  const int64_t nqb = (a.seq + QB - 1) / QB;
+  const int64_t grid = nqb * a.batch * a.heads;
+  if (grid > 0x7fffffff) return hipErrorInvalidConfiguration;
+  if (a.key_valid)
+    hipLaunchKernelGGL((attention_kernel<HD, QT, IT, OT, true>), dim3((unsigned)grid), dim3(kBlock), 0, s, a);
+  else
+    hipLaunchKernelGGL((attention_kernel<HD, QT, IT, OT, false>), dim3((unsigned)grid), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
+template <typename IT, typename OT>
+static hipError_t attn_dispatch(int variant, const AttnArgs& a, int hd, hipStream_t s) {
+  // variant 1: 16 queries per wave; variant 2: 32 queries per wave
+  const bool two = variant == 2;
+  switch (hd) {
+    case 16: return two ? launch_attn<16, 2, IT, OT>(a, s) : launch_attn<16, 1, IT, OT>(a, s);
+    case 32: return two ? launch_attn<32, 2, IT, OT>(a, s) : launch_attn<32, 1, IT, OT>(a, s);
+    case 64: return two ? launch_attn<64, 2, IT, OT>(a, s) : launch_attn<64, 1, IT, OT>(a, s);
+    case 128: return launch_attn<128, 1, IT, OT>(a, s);
+    default: return (hipError_t)MPK_EUNSUPPORTED;
+  }
+}
+
+}  // namespace mpk
+
+using namespace mpk;
+
+extern "C" int mpk_attention_auto_variant(int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim) {
+  (void)batch; (void)heads; (void)head_dim;
+  return seq_len >= 512 && head_dim <= 64 ? 2 : 1;
+}
+
+extern "C" int mpk_causal_attention(const void* q, const void* k, const void* v, void* o, int io_dtype,
+                                    int out_dtype, const int64_t* q_strides, const int64_t* k_strides,
+                                    const int64_t* v_strides, const int64_t* o_strides, int32_t batch,
+                                    int32_t heads, int32_t seq_len, int32_t head_dim, float scale, int causal,
+                                    const uint8_t* key_valid, int variant, void* stream) {
+  if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return MPK_EINVAL;
+  if (batch < 0 || heads <= 0 || seq_len < 0) return MPK_EINVAL;
+  if ((io_dtype != kF32 && io_dtype != kF16) || (out_dtype != kF32 && out_dtype != kF16)) return MPK_EINVAL;
+  if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128) return MPK_EUNSUPPORTED;
+  const int64_t* st[4] = {q_strides, k_strides, v_strides, o_strides};
+  const void* base[4] = {q, k, v, o};
+  for (int i = 0; i < 4; ++i) {
+    if (st[i][3] != 1) return MPK_EUNSUPPORTED;  // head-dim elements must be contiguous
+    const int esz = (i == 3 ? out_dtype : io_dtype) == kF32 ? 4 : 2;
+    if ((reinterpret_cast<uintptr_t>(base[i]) & 15u) != 0) return MPK_EALIGN;
+    for (int j = 0; j < 3; ++j)
+      if ((st[i][j] * esz) % 16 != 0) return MPK_EALIGN;
+  }
+  if (batch == 0 || seq_len == 0) return MPK_OK;
+  if (variant == 0) variant = mpk_attention_auto_variant(batch, heads, seq_len, head_dim);
+  if (variant != 1 && variant != 2) return MPK_EUNSUPPORTED;
+  AttnArgs a{};
+  a.q = q; a.k = k; a.v = v; a.o = o;
+  for (int j = 0; j < 4; ++j) {
+    a.qs[j] = q_strides[j]; a.ks[j] = k_strides[j]; a.vs[j] = v_strides[j]; a.os[j] = o_strides[j];
+  }
+  a.key_valid = key_valid;
+  a.batch = batch; a.heads = heads; a.seq = seq_len; a.causal = causal ? 1 : 0;
+  a.c = scale * 1.4426950408889634f;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (io_dtype == kF16)
+    e = out_dtype == kF16 ? attn_dispatch<_Float16, _Float16>(variant, a, head_dim, s)
+                          : attn_dispatch<_Float16, float>(variant, a, head_dim, s);
+  else
+    e = out_dtype == kF16 ? attn_dispatch<float, _Float16>(variant, a, head_dim, s)
+                          : attn_dispatch<float, float>(variant, a, head_dim, s);
+  return (int)e;
+}

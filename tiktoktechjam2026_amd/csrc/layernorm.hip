@@ -1,0 +1,147 @@
+// Residual-add + LayerNorm (FP32 statistics) and the plain initial LayerNorm.
+//
+// Replaces the reference's Triton row kernels
+//   _fused_add_layer_norm_kernel        torch_transformer_benchmark.py:37-69
+//   _add_layer_norm_mixed_output_kernel mixed_precision/triton_linear.py:188-218
+// and the initial nn.LayerNorm + cast at mixed_precision/transformer.py:484-486.
+//
+// r = x (+ u);  mean = sum(r)/d;  var = sum((r-mean)^2)/d  (biased, two-pass);
+// n = (r - mean) * rsqrt(var + eps) * gamma + beta.  r is written in FP32, n in
+// FP32 or FP16.  HBM-bound: one read of x (and u), one write of r and n.
+//
+// Layout: a group of G lanes owns one row; each lane holds NV float4 chunks
+// strided by G (so a group's loads are contiguous 16-byte chunks).  Row sums
+// are butterfly shuffles inside the group.
+#include "mpk_common.h"
+
+namespace mpk {
+
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, G);
+  return v;
+}
+
+template <int G, int NV, bool HAS_U, typename OT>
+__global__ __launch_bounds__(kBlock) void residual_layernorm_kernel(
+    const float* __restrict__ x, const float* __restrict__ u, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float* __restrict__ res_out, OT* __restrict__ norm_out, int64_t rows,
+    int d, float eps) {
+  const int lane = threadIdx.x % G;
+  const int64_t row = (int64_t)blockIdx.x * (kBlock / G) + threadIdx.x / G;
+  if (row >= rows) return;  // a whole group leaves together; shuffles stay inside the group
+  const int nvec = d >> 2;
+  const float* xr = x + row * d;
+  float4 r[NV];
+  float sum = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = lane + v * G;
+    if (c < nvec) {
+      float4 a = reinterpret_cast<const float4*>(xr)[c];
+      if (HAS_U) {
+        const float4 b = reinterpret_cast<const float4*>(u + row * d)[c];
+        a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+      }
+      r[v] = a;
+      sum += (a.x + a.y) + (a.z + a.w);
+    } else {
+      r[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  const float inv_d = 1.0f / (float)d;
+  const float mean = group_sum<G>(sum) * inv_d;
+  float sq = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = lane + v * G;
+    if (c < nvec) {
+      const float a = r[v].x - mean, b = r[v].y - mean, e = r[v].z - mean, f = r[v].w - mean;
+      sq += (a * a + b * b) + (e * e + f * f);
+    }
+  }
+  const float rstd = rsqrtf(group_sum<G>(sq) * inv_d + eps);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = lane + v * G;
+    if (c < nvec) {
+      if (HAS_U) reinterpret_cast<float4*>(res_out + row * d)[c] = r[v];
+      const float4 gm = reinterpret_cast<const float4*>(gamma)[c];
+      const float4 bt = reinterpret_cast<const float4*>(beta)[c];
+      float o[4];
+      o[0] = (r[v].x - mean) * rstd * gm.x + bt.x;
+      o[1] = (r[v].y - mean) * rstd * gm.y + bt.y;
+      o[2] = (r[v].z - mean) * rstd * gm.z + bt.z;
+      o[3] = (r[v].w - mean) * rstd * gm.w + bt.w;
+      OT* dst = norm_out + row * d + 4 * c;
+      if constexpr (sizeof(OT) == 4) {
+        *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+      } else {
+        h4 h;
+        h[0] = (_Float16)o[0]; h[1] = (_Float16)o[1]; h[2] = (_Float16)o[2]; h[3] = (_Float16)o[3];
+        *reinterpret_cast<h4*>(dst) = h;
+      }
+    }
+  }
+}
+
+template <int G, int NV, bool HAS_U, typename OT>
+static hipError_t launch_ln(const float* x, const float* u, const float* gamma, const float* beta,
+                            float* res_out, OT* norm_out, int64_t rows, int d, float eps, hipStream_t s) {
+  const int64_t rows_per_block = kBlock / G;
+  const int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL((residual_layernorm_kernel<G, NV, HAS_U, OT>), dim3((unsigned)blocks), dim3(kBlock), 0, s, x,
+                     u, gamma, beta, res_out, norm_out, rows, d, eps);
+  return hipGetLastError();
+}
+
+template <int G, int NV, typename OT>
+static hipError_t dispatch_u(const float* x, const float* u, const float* gamma, const float* beta, float* res_out,
+                             OT* norm_out, int64_t rows, int d, float eps, hipStream_t s) {
+  if (u) return launch_ln<G, NV, true, OT>(x, u, gamma, beta, res_out, norm_out, rows, d, eps, s);
+  return launch_ln<G, NV, false, OT>(x, u, gamma, beta, res_out, norm_out, rows, d, eps, s);
+}
+
+template <typename OT>
+static hipError_t dispatch_width(const float* x, const float* u, const float* gamma, const float* beta,
+                                 float* res_out, OT* norm_out, int64_t rows, int d, float eps, hipStream_t s) {
+  const int nvec = d / 4;
+  if (nvec <= 4) return dispatch_u<4, 1, OT>(x, u, gamma, beta, res_out, norm_out, rows, d, eps, s);
+  if (nvec <= 8) return dispatch_u<8, 1, OT>(x, u, gamma, beta, res_out, norm_out, rows, d, eps, s);
+  if (nvec <= 16) return dispatch_u<16, 1, OT>(x, u, gamma, beta, res_out, norm_out, rows, d, eps, s);
+  if (nvec <= 32) return dispatch_u<32, 1, OT>(x, u, gamma, beta, res_out, norm_out, rows, d, eps, s);
+  if (nvec <= 64) return dispatch_u<64, 1, OT>(x, u, gamma, beta, res_out, norm_out, rows, d, eps, s);
+  if (nvec <= 128) return dispatch_u<64, 2, OT>(x, u, gamma, beta, res_out, norm_out, rows, d, eps, s);
+  if (nvec <= 256) return dispatch_u<64, 4, OT>(x, u, gamma, beta, res_out, norm_out, rows, d, eps, s);
+  return dispatch_u<64, 8, OT>(x, u, gamma, beta, res_out, norm_out, rows, d, eps, s);
+}
+
+}  // namespace mpk
+
+using namespace mpk;
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// See include/mpk.h for the contract.
+extern "C" int mpk_layernorm(const float* x, const float* update, const float* gamma, const float* beta,
+                             float* residual_out, void* normalized_out, int normalized_dtype, int64_t rows,
+                             int32_t d, float eps, void* stream) {
+  if (!x || !gamma || !beta || !normalized_out || rows < 0) return MPK_EINVAL;
+  if (update && !residual_out) return MPK_EINVAL;
+  if (normalized_dtype != kF32 && normalized_dtype != kF16) return MPK_EINVAL;
+  if (d <= 0 || d % 4 != 0 || d > 2048) return MPK_EUNSUPPORTED;
+  if (!aligned16(x) || !aligned16(gamma) || !aligned16(beta) || (update && !aligned16(update)) ||
+      (residual_out && !aligned16(residual_out)) || !aligned16(normalized_out))
+    return MPK_EALIGN;
+  if (rows == 0) return MPK_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (normalized_dtype == kF32)
+    e = dispatch_width<float>(x, update, gamma, beta, residual_out, static_cast<float*>(normalized_out), rows, d,
+                              eps, s);
+  else
+    e = dispatch_width<_Float16>(x, update, gamma, beta, residual_out, static_cast<_Float16*>(normalized_out), rows,
+                                 d, eps, s);
+  return (int)e;
+}

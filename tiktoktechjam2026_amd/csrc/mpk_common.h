@@ -1,0 +1,123 @@
+// Shared device helpers for the gfx950 (CDNA4) mixed-precision Transformer kernels.
+//
+// Conventions used by every kernel in this library
+// ------------------------------------------------
+// * Wavefronts are 64 lanes.  A lane index l splits as r = l % 16 (MFMA row/col)
+//   and g = l / 16 (the lane group that owns a k-slice of an MFMA operand).
+// * All matrix products use v_mfma_f32_16x16x32_f16 (FP16 x FP16 -> FP32) or, for
+//   16-wide head dims, v_mfma_f32_16x16x16_f16.  Operand layouts (checked on the
+//   device by tests/test_kernels_gpu.py::test_mfma_lane_layout):
+//     A (16 x K): lane l holds row r, k = 8g .. 8g+7          (16x16x32)
+//     B (K x 16): lane l holds col r, k = 8g .. 8g+7
+//     C (16 x 16): lane l holds col r, rows 4g .. 4g+3
+//   The k -> slot assignment only has to agree between A and B, which lets a
+//   kernel feed one MFMA's result straight into the next one's B operand.
+// * "Transposed" products: every GEMM here computes C^T = W * X^T, i.e. the
+//   weight rows (output features n) are the MFMA rows and the token rows m are
+//   the MFMA columns.  A lane then owns one token row and a run of output
+//   features, which makes row-wise epilogues (bias, GELU, residual, LayerNorm)
+//   lane-local and gives 16-byte stores.
+// * "Paired" row mapping: two consecutive 16-row MFMA tiles (t = 0, 1) cover 32
+//   output features; MFMA row q of tile t is mapped to feature
+//       pair_row(q, t) = 8 * (q / 4) + 4 * t + (q % 4)
+//   so lane group g ends up holding features 8g .. 8g+7 of the pair in one
+//   contiguous run: acc[t][i] is feature 8g + 4t + i.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mpk.h"  // the exported C ABI (include/mpk.h); definitions are checked against it
+
+namespace mpk {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+enum DType : int { kF32 = 0, kF16 = 1 };
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;  // four waves per workgroup everywhere
+
+__device__ __forceinline__ f4 mfma32(const h8& a, const h8& b, const f4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f4 mfma16(const h4& a, const h4& b, const f4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int pair_row(int q, int t) { return 8 * (q >> 2) + 4 * t + (q & 3); }
+
+__device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
+
+// ---- global loads of 8 consecutive elements as FP16 (round-to-nearest-even) ----
+__device__ __forceinline__ h8 load8_as_half(const _Float16* p) { return *reinterpret_cast<const h8*>(p); }
+
+__device__ __forceinline__ h8 load8_as_half(const float* p) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  h8 r;
+  r[0] = (_Float16)a.x; r[1] = (_Float16)a.y; r[2] = (_Float16)a.z; r[3] = (_Float16)a.w;
+  r[4] = (_Float16)b.x; r[5] = (_Float16)b.y; r[6] = (_Float16)b.z; r[7] = (_Float16)b.w;
+  return r;
+}
+
+__device__ __forceinline__ h8 zero_h8() {
+  h8 r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = (_Float16)0.f;
+  return r;
+}
+
+__device__ __forceinline__ void load8_f32(const float* p, float* v) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+__device__ __forceinline__ void load8_f16_to_f32(const _Float16* p, float* v) {
+  const h8 h = *reinterpret_cast<const h8*>(p);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = (float)h[j];
+}
+
+// ---- stores of 8 consecutive FP32 values, as FP32 or rounded to FP16 ----
+__device__ __forceinline__ void store8(float* p, const float* v) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+__device__ __forceinline__ void store8(_Float16* p, const float* v) {
+  h8 h;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) h[j] = (_Float16)v[j];
+  *reinterpret_cast<h8*>(p) = h;
+}
+
+// Exact (erf-based) GELU in FP32: 0.5 v (1 + erf(v / sqrt(2))).
+__device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+
+// Sum over the four lane groups g that share one MFMA column (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ float sum_over_groups(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+__device__ __forceinline__ float max_over_groups(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+// Map a linear workgroup id so that consecutive tile indices land on the same
+// XCD (workgroups are dispatched round-robin over the 8 XCDs, each with its own
+// L2).  Identity when the grid is not a multiple of 8.
+__device__ __forceinline__ int xcd_local_tile(int wg, int nwg) {
+  if ((nwg & 7) != 0) return wg;
+  return (wg & 7) * (nwg >> 3) + (wg >> 3);
+}
+
+}  // namespace mpk

@@ -1,0 +1,117 @@
+"""Shape-dispatch table for the HIP forward (replaces the reference's exact-shape route flags).
+
+The reference selects Triton routes with hard-coded exact-shape booleans
+(``mixed_precision/transformer.py:337-448``) and per-row-count tile tables
+(``:88-99, :198-205, :518-560``); any shape outside them falls back to vendor
+ops.  Here every supported shape takes the same HIP route; what varies with
+the shape is only
+
+* which fusions apply (the fused out-projection/FFN kernels cover
+  d_model in {32, 64, 128, 256, 512}; other widths use the unfused HIP
+  projection + residual-LayerNorm kernels), and
+* the kernel tile variant of each launch.  Variant 0 defers to the
+  library's built-in table (``mpk_*_auto_variant``); entries in ``TUNED``
+  override it for shapes measured on MI355X (256 CUs, 64-lane waves).
+
+Tile variants (see the kernel sources for the exact tiles):
+  qkv / ffn-in projection  1: 128x128 (2x2 waves)  2: 128x64  3: 128x32  4: 64x128
+  out-proj + LN            1: 64 rows/WG           2: 128 rows/WG (d <= 128)
+  fused FFN + LN           1: 16 rows/wave         2: 32 rows/wave (d <= 256)
+  attention                1: 16 queries/wave      2: 32 queries/wave (hd <= 64)
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field, replace
+from typing import Dict, Tuple
+
+import torch
+
+LN_FUSED_WIDTHS = (32, 64, 128, 256, 512)
+ATTENTION_HEAD_DIMS = (16, 32, 64, 128)
+
+
+@dataclass(frozen=True)
+class Route:
+    """Everything the forward needs to know about how to run one configuration."""
+
+    supported: bool
+    reason: str
+    normalized_dtype: torch.dtype = torch.float16
+    fp16_attention: bool = True
+    fuse_attention_output_norm: bool = True
+    fuse_full_ffn: bool = True
+    qkv_variant: int = 0
+    attention_variant: int = 0
+    out_ln_variant: int = 0
+    ffn_variant: int = 0
+    ffn_in_variant: int = 0
+    ffn_out_variant: int = 0
+    notes: Tuple[str, ...] = field(default_factory=tuple)
+
+    def describe(self) -> Dict[str, object]:
+        return {
+            "supported": self.supported,
+            "reason": self.reason,
+            "normalized_stream": "fp16" if self.normalized_dtype == torch.float16 else "fp32",
+            "attention": "hip_fp16_flash" if self.fp16_attention else "hip_fp32io_flash",
+            "attention_output_norm_fusion": self.fuse_attention_output_norm,
+            "full_ffn_fusion": self.fuse_full_ffn,
+            "variants": {
+                "qkv": self.qkv_variant,
+                "attention": self.attention_variant,
+                "out_ln": self.out_ln_variant,
+                "ffn": self.ffn_variant,
+                "ffn_in": self.ffn_in_variant,
+                "ffn_out": self.ffn_out_variant,
+            },
+        }
+
+
+def _token_bucket(tokens: int) -> str:
+    if tokens < 16384:
+        return "small"
+    if tokens < 131072:
+        return "medium"
+    return "large"
+
+
+# (d_model, ffn_dim, num_heads, token bucket) -> variant overrides, from MI355X measurements.
+TUNED: Dict[Tuple[int, int, int, str], Dict[str, int]] = {}
+
+
+def plan(
+    config,
+    *,
+    enable_attention_output_norm_fusion: bool = True,
+    enable_full_ffn_fusion: bool = True,
+    enable_fp16_custom_attention: bool = True,
+    enable_fp16_normalized_stream: bool = True,
+) -> Route:
+    """Return the route for ``config`` (any object with the TransformerConfig fields)."""
+    d = int(config.d_model)
+    f = int(config.ffn_dim)
+    h = int(config.num_heads)
+    if h <= 0 or d % h != 0:
+        return Route(False, "d_model must be divisible by num_heads")
+    hd = d // h
+    if hd not in ATTENTION_HEAD_DIMS:
+        return Route(False, f"head_dim {hd} not in {ATTENTION_HEAD_DIMS}")
+    if d % 8 != 0 or f % 8 != 0:
+        return Route(False, "d_model and ffn_dim must be multiples of 8")
+    if d > 2048:
+        return Route(False, "d_model above 2048")
+    fuse_out = enable_attention_output_norm_fusion and d in LN_FUSED_WIDTHS
+    fuse_ffn = enable_full_ffn_fusion and d in LN_FUSED_WIDTHS and f % 32 == 0
+    route = Route(
+        True,
+        "hip",
+        normalized_dtype=torch.float16 if enable_fp16_normalized_stream else torch.float32,
+        fp16_attention=enable_fp16_custom_attention,
+        fuse_attention_output_norm=fuse_out,
+        fuse_full_ffn=fuse_ffn,
+    )
+    tuned = TUNED.get((d, f, h, _token_bucket(int(config.batch_size) * int(config.seq_len))))
+    if tuned:
+        route = replace(route, **tuned)
+    return route

@@ -1,0 +1,243 @@
+"""Mixed FP16/FP32 causal Transformer forward running on hand-written gfx950 HIP kernels.
+
+Drop-in for the reference's ``mixed_precision/transformer.py``:
+``MixedPrecisionTransformer`` (:322-694), ``MixedPrecisionTransformerBlock``
+(:276-319), ``MixedPrecisionSelfAttention`` (:34-273) and
+``copy_mixed_model_weights`` (:697-726) keep their constructor keywords, the
+attributes the benchmark CLI reads, the state-dict keys and dtypes
+(packed ``qkv_proj`` ``[3D, D]``; FP16 projection weights/biases after
+``convert_projections_to_fp16``; FP32 LayerNorm parameters) and the
+``forward(x fp32 [B,S,D], valid_token_mask=None) -> fp32 [B,S,D]`` contract
+(``ValueError`` for non-FP32 input).
+
+Per layer the forward issues four HIP launches (the reference issues four
+Triton launches on its D128 routes and vendor ops elsewhere):
+
+  1. packed QKV projection          fp16 stream -> fp16 [T, 3D]        (mpk_linear)
+  2. causal flash attention         strided q/k/v -> fp16 [T, D]       (mpk_causal_attention)
+  3. out-projection + residual + LN -> fp32 residual, fp16 normalized (mpk_linear_residual_layernorm)
+  4. FFN + residual + next LN       -> fp32 residual, fp16 normalized (mpk_ffn_residual_layernorm)
+
+plus one initial LayerNorm.  The last layer's normalized output is FP32 (it is
+the model output).  Rounding points: GEMM operands FP16, accumulation / bias /
+GELU / residual / LayerNorm statistics FP32, attention probabilities FP16 only
+for the P.V product - the same points as the reference's FP16 route.
+"""
+
+from __future__ import annotations
+
+import copy
+from typing import Dict, Mapping, Optional, Union
+
+import torch
+import torch.nn as nn
+
+from .. import dispatch
+from ..custom_kernel.hip_attention import attention
+from .hip_linear import (
+    layer_norm,
+    mixed_add_layer_norm,
+    mixed_ffn_add_layer_norm,
+    mixed_linear,
+    mixed_linear_add_layer_norm,
+)
+
+
+class MixedPrecisionSelfAttention(nn.Module):
+    """Packed-QKV self-attention; parameters ``qkv_proj [3D, D]`` and ``out_proj [D, D]``."""
+
+    def __init__(self, d_model: int, num_heads: int, route: dispatch.Route) -> None:
+        super().__init__()
+        self.d_model = d_model
+        self.num_heads = num_heads
+        self.head_dim = d_model // num_heads
+        self.scale = self.head_dim ** -0.5
+        self.route = route
+        self.qkv_proj = nn.Linear(d_model, 3 * d_model, bias=True)
+        self.out_proj = nn.Linear(d_model, d_model, bias=True)
+
+    def convert_projections_to_fp16(self) -> None:
+        self.qkv_proj.half()
+        self.out_proj.half()
+
+    def context(
+        self,
+        normalized: torch.Tensor,
+        key_valid: Optional[torch.Tensor],
+        causal: bool,
+    ) -> torch.Tensor:
+        """QKV projection + flash attention -> context ``[B, S, D]`` (fp16, or fp32 on the fp32-I/O route)."""
+        batch, seq_len, _ = normalized.shape
+        route = self.route
+        qkv_dtype = torch.float16 if route.fp16_attention else torch.float32
+        qkv = mixed_linear(normalized, self.qkv_proj, output_dtype=qkv_dtype, variant=route.qkv_variant)
+        q, k, v = qkv.view(batch, seq_len, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
+        ctx = attention(q, k, v, self.scale, causal=causal, key_valid=key_valid, variant=route.attention_variant)
+        return ctx.view(batch, seq_len, self.d_model)
+
+    def forward(
+        self,
+        normalized: torch.Tensor,
+        valid_token_mask: Optional[torch.Tensor] = None,
+        causal: bool = False,
+        residual_fp32: Optional[torch.Tensor] = None,
+        next_norm: Optional[nn.LayerNorm] = None,
+    ) -> Union[torch.Tensor, tuple]:
+        """Attention sub-block.  With ``residual_fp32`` and ``next_norm`` returns ``(x', LN(x'))``
+        (the fused out-projection + residual + LayerNorm); otherwise the FP32 projection output."""
+        ctx = self.context(normalized, valid_token_mask, causal)
+        route = self.route
+        if residual_fp32 is not None and next_norm is not None:
+            if route.fuse_attention_output_norm:
+                return mixed_linear_add_layer_norm(
+                    ctx, self.out_proj, residual_fp32, next_norm,
+                    normalized_dtype=route.normalized_dtype, variant=route.out_ln_variant,
+                )
+            projected = mixed_linear(ctx, self.out_proj, output_dtype=torch.float32)
+            return mixed_add_layer_norm(residual_fp32, projected, next_norm, normalized_dtype=route.normalized_dtype)
+        return mixed_linear(ctx, self.out_proj, output_dtype=torch.float32)
+
+
+class MixedPrecisionTransformerBlock(nn.Module):
+    def __init__(self, d_model: int, num_heads: int, ffn_dim: int, route: dispatch.Route) -> None:
+        super().__init__()
+        self.norm1 = nn.LayerNorm(d_model)
+        self.attention = MixedPrecisionSelfAttention(d_model, num_heads, route)
+        self.norm2 = nn.LayerNorm(d_model)
+        self.ffn_in = nn.Linear(d_model, ffn_dim)
+        self.ffn_out = nn.Linear(ffn_dim, d_model)
+        self.route = route
+        self.fuse_attention_output_norm = route.fuse_attention_output_norm
+        self.fuse_full_ffn = route.fuse_full_ffn
+
+    def convert_projections_to_fp16(self) -> None:
+        self.attention.convert_projections_to_fp16()
+        self.ffn_in.half()
+        self.ffn_out.half()
+
+    def ffn(
+        self, normalized_ffn: torch.Tensor, residual: torch.Tensor, next_norm: nn.LayerNorm, out_dtype: torch.dtype
+    ):
+        """FFN + residual + next LayerNorm -> ``(x', next_norm(x'))``."""
+        route = self.route
+        if route.fuse_full_ffn:
+            return mixed_ffn_add_layer_norm(
+                normalized_ffn, self.ffn_in, self.ffn_out, residual, next_norm,
+                normalized_dtype=out_dtype, variant=route.ffn_variant,
+            )
+        activated = mixed_linear(
+            normalized_ffn, self.ffn_in, output_dtype=torch.float16, fuse_gelu=True, variant=route.ffn_in_variant
+        )
+        if self.ffn_out.in_features == self.ffn_out.out_features and route.fuse_attention_output_norm:
+            return mixed_linear_add_layer_norm(
+                activated, self.ffn_out, residual, next_norm, normalized_dtype=out_dtype, variant=route.out_ln_variant
+            )
+        projected = mixed_linear(activated, self.ffn_out, output_dtype=torch.float32, variant=route.ffn_out_variant)
+        return mixed_add_layer_norm(residual, projected, next_norm, normalized_dtype=out_dtype)
+
+
+class MixedPrecisionTransformer(nn.Module):
+    """FP16 MFMA projections and attention with FP32 accumulation, residual stream and LayerNorm."""
+
+    def __init__(
+        self,
+        config,
+        *,
+        enable_case11_schedule: bool = True,
+        enable_attention_output_norm_fusion: bool = True,
+        enable_full_ffn_fusion: bool = True,
+        enable_fp16_custom_attention: bool = True,
+        enable_fp16_normalized_stream: bool = True,
+    ) -> None:
+        super().__init__()
+        self.config = config
+        route = dispatch.plan(
+            config,
+            enable_attention_output_norm_fusion=enable_attention_output_norm_fusion,
+            enable_full_ffn_fusion=enable_full_ffn_fusion,
+            enable_fp16_custom_attention=enable_fp16_custom_attention,
+            enable_fp16_normalized_stream=enable_fp16_normalized_stream,
+        )
+        if not route.supported:
+            raise ValueError(f"unsupported configuration for the HIP forward: {route.reason}")
+        self.route = route
+        # Route attributes read by the benchmark CLI (mixed_precision_benchmark.py:67-77 in the
+        # reference).  They now describe the HIP route: every projection runs on HIP MFMA kernels
+        # and attention is the HIP flash kernel; the Triton special cases do not exist.
+        self.use_case8_triton = False
+        self.use_d32_triton = False
+        self.use_d128_triton = True
+        self.use_fp16_custom_attention = route.fp16_attention
+        self.use_d128_custom_attention = not route.fp16_attention
+        self.use_case11_schedule = False
+        self.fuse_attention_output_norm = route.fuse_attention_output_norm
+        self.fuse_full_ffn = route.fuse_full_ffn
+        self.use_fp16_normalized_stream = route.normalized_dtype == torch.float16
+        self.layers = nn.ModuleList(
+            [
+                MixedPrecisionTransformerBlock(config.d_model, config.num_heads, config.ffn_dim, route)
+                for _ in range(config.num_layers)
+            ]
+        )
+        self.final_norm = nn.LayerNorm(config.d_model)
+        self.assume_all_tokens_valid = False
+
+    def convert_projections_to_fp16(self) -> None:
+        for layer in self.layers:
+            layer.convert_projections_to_fp16()
+
+    def dispatch_report(self) -> Dict[str, object]:
+        return self.route.describe()
+
+    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if x.dtype != torch.float32:
+            raise ValueError("mixed candidate requires an FP32 input/residual stream")
+        if not x.is_cuda:
+            raise ValueError("the HIP forward requires a GPU input tensor")
+        effective_mask = None if self.assume_all_tokens_valid else valid_token_mask
+        causal = bool(self.config.causal)
+        stream_dtype = self.route.normalized_dtype
+        n_layers = len(self.layers)
+
+        normalized = layer_norm(x, self.layers[0].norm1, normalized_dtype=stream_dtype)
+        for index, layer in enumerate(self.layers):
+            x, normalized_ffn = layer.attention(
+                normalized, effective_mask, causal, residual_fp32=x, next_norm=layer.norm2
+            )
+            last = index + 1 == n_layers
+            next_norm = self.final_norm if last else self.layers[index + 1].norm1
+            x, normalized = layer.ffn(normalized_ffn, x, next_norm, torch.float32 if last else stream_dtype)
+
+        if effective_mask is not None:
+            return normalized.masked_fill(~effective_mask[..., None], 0)
+        return normalized
+
+
+def _source_state(baseline: Union[nn.Module, Mapping[str, torch.Tensor]]) -> Dict[str, torch.Tensor]:
+    if isinstance(baseline, Mapping):
+        return {k: v.detach().clone() for k, v in baseline.items()}
+    return copy.deepcopy(dict(baseline.state_dict()))
+
+
+def copy_mixed_model_weights(
+    baseline: Union[nn.Module, Mapping[str, torch.Tensor]], mixed: MixedPrecisionTransformer
+) -> None:
+    """Copy strict-FP32 reference weights into ``mixed``, packing q/k/v into ``qkv_proj``.
+
+    ``baseline`` is a module whose ``state_dict()`` has the reference keys
+    (``layers.{i}.attention.q_proj.weight`` ...) or such a dict.  Loaded strictly.
+    """
+    source = _source_state(baseline)
+    mapped = {}
+    for key in mixed.state_dict():
+        for kind in ("weight", "bias"):
+            suffix = f"attention.qkv_proj.{kind}"
+            if key.endswith(suffix):
+                prefix = key[: -len(f"qkv_proj.{kind}")]
+                mapped[key] = torch.cat(
+                    [source[prefix + f"{n}_proj.{kind}"] for n in ("q", "k", "v")], dim=0
+                )
+                break
+        else:
+            mapped[key] = source[key]
+    mixed.load_state_dict(mapped, strict=True)
