@@ -108,6 +108,38 @@ int mpk_causal_attention(const void* q, const void* k, const void* v, void* o, i
                          void* stream);
 int mpk_attention_auto_variant(int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim);
 
+/*
+ * Whole-layer tail for narrow models: everything after attention up to the next
+ * layer's QKV projection, with the activations kept on chip:
+ *   x_out = fp16(ctx) w_o^T + b_o + x                               (FP32)
+ *   n2    = LayerNorm(x_out; ln2_w, ln2_b, ln2_eps)                 (FP16 operand)
+ *   x_out = fp16(GELU_erf(n2 w_in^T + b_in)) w_out^T + b_out + x_out (FP32)
+ *   last == 0: out = LayerNorm(x_out; next_ln) w_qkv^T + b_qkv      (FP16 [m, 3d])
+ *   last != 0: out = LayerNorm(x_out; next_ln)                      (FP32 [m, d])
+ * ctx: [m, d] FP16; x, x_out: [m, d] FP32 (may not alias); w_o [d, d], w_in [f, d],
+ * w_out [d, f], w_qkv [3d, d] and their biases FP16; LayerNorm parameters FP32.
+ * (d, f) must satisfy mpk_layer_tail_supported.
+ * Replaces, fused: mixed_linear_add_layer_norm + mixed_ffn_add_layer_norm +
+ * the next layer's mixed_linear QKV call (mixed_precision/transformer.py:196-222,
+ * :540-560, :88-120); no single reference function corresponds to it.
+ */
+int mpk_layer_tail(const void* ctx, const float* x, const void* w_o, const void* b_o, const float* ln2_w,
+                   const float* ln2_b, const void* w_in, const void* b_in, const void* w_out, const void* b_out,
+                   const float* next_ln_w, const float* next_ln_b, const void* w_qkv, const void* b_qkv,
+                   float* x_out, void* out, int last, int64_t m, int32_t d, int32_t f, float ln2_eps,
+                   float next_ln_eps, int variant, void* stream);
+int mpk_layer_tail_supported(int32_t d, int32_t f);
+
+/*
+ * First-layer head: qkv = LayerNorm(x; ln_w, ln_b, eps) w_qkv^T + b_qkv.
+ * x: [m, d] FP32; w_qkv: [3d, d] FP16; b_qkv: [3d] FP16; qkv: [m, 3d] FP16.
+ * Replaces, fused: the initial norm1 + cast (mixed_precision/transformer.py:484-486)
+ * and the first layer's QKV mixed_linear (:88-120).
+ */
+int mpk_layernorm_qkv(const float* x, const float* ln_w, const float* ln_b, const void* w_qkv,
+                      const void* b_qkv, void* qkv, int64_t m, int32_t d, float eps, int variant, void* stream);
+int mpk_layernorm_qkv_supported(int32_t d);
+
 #ifdef __cplusplus
 }
 #endif

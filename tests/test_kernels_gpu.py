@@ -284,3 +284,65 @@ def test_attention_rejects_unsupported(hip_device):
     assert not is_fp16_supported(x, x, x, True)
     with pytest.raises(ValueError):
         attention(x, x, x, 1.0)
+
+
+# --------------------------------------------------------------------------- whole-layer fusions
+
+
+def _ln_module_ref(r64, norm):
+    return _ln64(r64, norm)
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("m", [5, 1000, 9000])
+@pytest.mark.parametrize("variant", [1, 2])
+def test_layer_norm_qkv(hip_device, d, m, variant):
+    from tiktoktechjam2026_amd.mixed_precision.hip_fused import layer_norm_qkv
+
+    x = _randn((m, d), 51, 2.0)
+    norm = _norm(d, hip_device, 52)
+    lin = _linear(d, 3 * d, hip_device, 53)
+    qkv = layer_norm_qkv(x.to(hip_device), norm, lin, variant=variant)
+    assert qkv.dtype == torch.float16 and qkv.shape == (m, 3 * d)
+    n16 = _ln64(x.double(), norm).float().half()
+    ref = n16.double() @ lin.weight.detach().cpu().double().t() + lin.bias.detach().cpu().double()
+    # an FP16 rounding flip of a normalized value moves an output by <= ulp * |w|
+    _close(qkv, ref, 2 ** -9, 2 ** -10, "layer_norm_qkv")
+
+
+@pytest.mark.parametrize("d,f", [(128, 128), (32, 64), (64, 256), (32, 32)])
+@pytest.mark.parametrize("m", [7, 4100])
+@pytest.mark.parametrize("last", [False, True])
+@pytest.mark.parametrize("variant", [1, 2])
+def test_fused_layer_tail(hip_device, d, f, m, last, variant):
+    from tiktoktechjam2026_amd.mixed_precision.hip_fused import fused_layer_tail
+
+    ctx = _randn((m, d), 61)
+    x = _randn((m, d), 62, 2.0)
+    out_proj = _linear(d, d, hip_device, 63)
+    ffn_in = _linear(d, f, hip_device, 64)
+    ffn_out = _linear(f, d, hip_device, 65)
+    norm2 = _norm(d, hip_device, 66)
+    next_norm = _norm(d, hip_device, 67)
+    qkv_proj = None if last else _linear(d, 3 * d, hip_device, 68)
+    x_out, out = fused_layer_tail(
+        ctx.to(hip_device, torch.float16), x.to(hip_device), out_proj, norm2, ffn_in, ffn_out, next_norm, qkv_proj,
+        variant=variant,
+    )
+    W = lambda lin: lin.weight.detach().cpu().double()  # noqa: E731
+    B = lambda lin: lin.bias.detach().cpu().double()  # noqa: E731
+    x1 = ctx.half().double() @ W(out_proj).t() + B(out_proj) + x.double()
+    n2 = _ln64(x1, norm2).float().half().double()
+    h = n2 @ W(ffn_in).t() + B(ffn_in)
+    h = (0.5 * h * (1.0 + torch.erf(h / math.sqrt(2.0)))).float().half().double()
+    x2 = h @ W(ffn_out).t() + B(ffn_out) + x1
+    # FP16 rounding flips of n2 / h against the float64 chain bound the residual error
+    _close(x_out, x2, 3e-3, 1e-4, "layer tail residual")
+    n1 = _ln64(x2, next_norm)
+    if last:
+        assert out.dtype == torch.float32 and out.shape == (m, d)
+        _close(out, n1, 5e-3, 5e-3, "layer tail final norm")
+    else:
+        assert out.dtype == torch.float16 and out.shape == (m, 3 * d)
+        ref = n1.float().half().double() @ W(qkv_proj).t() + B(qkv_proj)
+        _close(out, ref, 5e-3, 5e-3, "layer tail qkv")

@@ -130,3 +130,23 @@ def test_hip_graph_replays_match_eager(hip_device):
             replay = graphed(x, None).clone()
         torch.cuda.synchronize()
         assert torch.equal(eager, replay), f"replay {seed} differs from eager"
+
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg3"])
+def test_layer_tail_route_matches_per_op_route(hip_device, name):
+    """The fused 1+2L-launch route and the per-operator route agree (same rounding points)."""
+    config = BENCHMARK_CONFIGS[name]
+    state = strict_fp32.seeded_state_dict(config, 1234)
+    fused = MixedPrecisionTransformer(config)
+    assert fused.route.fuse_layer_tail
+    per_op = MixedPrecisionTransformer(config)
+    per_op.route = dataclasses.replace(per_op.route, fuse_layer_tail=False)
+    for model in (fused, per_op):
+        copy_mixed_model_weights(state, model)
+        model.to(hip_device).eval()
+        model.convert_projections_to_fp16()
+    x, _ = harness.generate_random_case(config, hip_device, torch.float32, 31, 0.0, 1.0)
+    with torch.inference_mode():
+        a = fused(x)
+        b = per_op(x)
+    assert float((a - b).abs().max()) < 1e-3

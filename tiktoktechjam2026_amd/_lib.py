@@ -69,6 +69,20 @@ SIGNATURES = {
         ],
     ),
     "mpk_attention_auto_variant": (_c_int, [_c_i32, _c_i32, _c_i32, _c_i32]),
+    "mpk_layer_tail": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i32,
+            _c_i32, _c_float, _c_float, _c_int, _c_void_p,
+        ],
+    ),
+    "mpk_layer_tail_supported": (_c_int, [_c_i32, _c_i32]),
+    "mpk_layernorm_qkv": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i32, _c_float, _c_int, _c_void_p],
+    ),
+    "mpk_layernorm_qkv_supported": (_c_int, [_c_i32]),
 }
 
 _lock = threading.Lock()

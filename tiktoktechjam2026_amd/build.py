@@ -34,6 +34,9 @@ COMMON_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep MFMA accumulators in ordinary VGPRs (no AGPR copies around the
+    # VALU epilogues and softmax that consume them)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE_DIR}",
     f"-I{CSRC_DIR}",
 ]

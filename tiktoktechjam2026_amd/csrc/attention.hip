@@ -6,7 +6,7 @@
 //   _causal_attention_fwd       custom_kernel/triton_attention.py:16-123   (FP32 I/O)
 // Math per query row (same rounding points as the FP16 reference kernel):
 //   s_j = q . k_j  (FP16 operands, FP32 accumulate)
-//   m   = running max of s (FP32);  p_j = 2^(s_j*c - m*c), c = scale*log2(e)
+//   m   = running max of s (FP32, raised lazily);  p_j = 2^(s_j*c - m*c), c = scale*log2(e)
 //   l   = running sum of p_j in FP32;  acc += fp16(p_j) * v_j  (FP32 accumulate)
 //   o   = acc / l, rounded to the output type.
 // For FP32 inputs (the reference's TF32 kernel) q, k, v are rounded to FP16 on
@@ -26,6 +26,10 @@
 namespace mpk {
 
 constexpr int KT = 64;  // keys per tile
+// Initial running max: finite so that a row whose keys are all masked so far
+// still gives exp2(-inf - kNoMax*c) = 0 instead of NaN.
+constexpr float kNoMax = -1.0e30f;
+constexpr float kRescaleLog2 = 8.0f;
 
 struct AttnArgs {
   const void* q;
@@ -106,7 +110,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
   f4 oacc[QT][SH::DT][2];
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
-    m_run[t] = -INFINITY;
+    m_run[t] = kNoMax;
     l_run[t] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < SH::DT; ++dt) oacc[t][dt][0] = oacc[t][dt][1] = zero4();
@@ -158,7 +162,8 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
     if (tile + 1 < ntiles) fetch(kb + KT);
 
     if (a.causal && kb > qw_last) continue;  // whole tile is in this wave's future
-    const bool need_mask = KEYMASK || kb + KT > S || (a.causal && kb + KT - 1 > qw0);
+    const bool need_causal = a.causal && kb + KT - 1 > qw0;  // tile straddles this wave's diagonal
+    const bool need_bias = KEYMASK || kb + KT > S;          // padded keys or keys past the end
 
     // ---- S^T = K Q^T for 64 keys x 16*QT queries ----
     f4 sc[2][2][QT];  // [key pair][tile in pair][q tile]
@@ -184,24 +189,32 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
       }
 
     // ---- online softmax, per query tile ----
+    // The running max is only raised when the tile max exceeds it by more than
+    // kRescaleLog2 (log2 units); otherwise the stale max is kept and p may reach
+    // 2^kRescaleLog2.  acc and l carry the same scale, so o = acc / l is unchanged.
     h8 pf[QT][2];  // fp16(P) as the B operand of the PV product, per key pair
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-      const int q = qw0 + 16 * t + r;
-      if (need_mask) {
+      if (need_causal) {
+        // key kb + 32p + 8g + 4tt + i is visible iff it is <= query qw0 + 16t + r
+        const int lim = qw0 + 16 * t + r - kb - 8 * g;
 #pragma unroll
         for (int p = 0; p < 2; ++p)
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int kl = 32 * p + 8 * g + 4 * tt + i;
-              float s = sc[p][tt][t][i] + kbias[kl];
-              if (a.causal && kb + kl > q) s = -INFINITY;
-              sc[p][tt][t][i] = s;
-            }
+            for (int i = 0; i < 4; ++i)
+              if (32 * p + 4 * tt + i > lim) sc[p][tt][t][i] = -INFINITY;
       }
-      float mx = -INFINITY;
+      if (need_bias) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[p][tt][t][i] += kbias[32 * p + 8 * g + 4 * tt + i];
+      }
+      float mx = sc[0][0][t][0];
 #pragma unroll
       for (int p = 0; p < 2; ++p)
 #pragma unroll
@@ -209,11 +222,18 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[p][tt][t][i]);
       mx = max_over_groups(mx);
-      const float m_new = fmaxf(m_run[t], mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f((m_run[t] - m_use) * a.c);
-      m_run[t] = m_new;
-      const float moff = -m_use * a.c;
+      const float m_cand = fmaxf(m_run[t], mx);
+      if ((m_cand - m_run[t]) * a.c > kRescaleLog2) {
+        const float alpha = __builtin_amdgcn_exp2f((m_run[t] - m_cand) * a.c);
+        m_run[t] = m_cand;
+        l_run[t] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < SH::DT; ++dt) {
+          oacc[t][dt][0] *= alpha;
+          oacc[t][dt][1] *= alpha;
+        }
+      }
+      const float moff = -m_run[t] * a.c;
       float psum = 0.f;
 #pragma unroll
       for (int p = 0; p < 2; ++p)
@@ -225,12 +245,7 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
             psum += pv;
             pf[t][p][4 * tt + i] = (_Float16)pv;
           }
-      l_run[t] = l_run[t] * alpha + psum;
-#pragma unroll
-      for (int dt = 0; dt < SH::DT; ++dt) {
-        oacc[t][dt][0] *= alpha;
-        oacc[t][dt][1] *= alpha;
-      }
+      l_run[t] += psum;
     }
 
     // ---- O^T += V^T P^T ----

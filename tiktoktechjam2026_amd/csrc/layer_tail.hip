@@ -1,0 +1,528 @@
+// Whole-layer tail fusion for narrow models (gfx950).
+//
+// Everything in a pre-LN block after attention is token-local, so one kernel
+// takes the attention context of a row tile all the way to the next layer's
+// packed QKV projection:
+//
+//   x'  = fp16(ctx) Wo^T + bo + x                      (FP32)
+//   n2  = LN2(x')                                      (FP32 stats, FP16 operand)
+//   x'' = fp16(GELU_erf(n2 Win^T + bin)) Wout^T + bout + x'    (FP32)
+//   n1  = LN1_next(x'')                                (FP32 stats, FP16 operand)
+//   qkv = n1 Wqkv_next^T + bqkv_next                   (FP32 accumulate, FP16 store)
+//   (last layer: out = LN_final(x'') in FP32 instead of n1 / qkv)
+//
+// This is the composition of the reference's kernels
+//   _mixed_linear_add_layer_norm_kernel (mixed_precision/triton_linear.py:72-125),
+//   _mixed_ffn_add_layer_norm_kernel    (:128-185) and
+//   _mixed_linear_kernel                (:16-69, the next layer's QKV projection)
+// with exactly the same rounding points; only x'' and qkv (or the final
+// output) are written to HBM.  A second entry runs just the last stage for the
+// first layer (x -> LN1 -> QKV).
+//
+// Structure.  Row-owner design: each wave owns 16*TM token rows for the whole
+// chain.  Every product is computed transposed with the paired row mapping
+// (mpk_common.h), so each stage's output, after its epilogue, is already the
+// FP16 B operand of the next product - activations never leave the register
+// file.  Wo, Win and Wout are loaded into LDS once per (persistent) workgroup;
+// the QKV weights live in LDS when they fit, otherwise each wave streams its
+// A fragments from L2.  Workgroups have 8 waves (2 per SIMD) sharing one copy
+// of the weights.
+#include <atomic>
+
+#include "mpk_common.h"
+
+namespace mpk {
+
+struct TailArgs {
+  const _Float16* ctx;  // [M, D] attention context (stage 1 only)
+  const float* x;       // [M, D] residual stream in
+  const _Float16* wo;   // [D, D]
+  const _Float16* bo;   // [D]
+  const float* g2;      // LN2 gamma / beta
+  const float* be2;
+  const _Float16* win;   // [F, D]
+  const _Float16* bin;   // [F]
+  const _Float16* wout;  // [D, F]
+  const _Float16* bout;  // [D]
+  const float* g1;       // next LayerNorm (LN1 of the next layer, or the final norm)
+  const float* be1;
+  const _Float16* wqkv;  // [3D, D] next layer's packed QKV (unless LAST)
+  const _Float16* bqkv;  // [3D]
+  float* x_out;          // [M, D] residual stream out (stage 1 only)
+  void* out;             // qkv FP16 [M, 3D], or final normalized FP32 [M, D] when LAST
+  int64_t m;
+  int f;
+  float eps2, eps1;
+};
+
+constexpr int kTailWaves = 8;
+constexpr int kTailThreads = 64 * kTailWaves;
+constexpr int kLdsBudget = 160 * 1024;
+
+// Where the next layer's QKV weights live.
+//   kQkvLds: in LDS; every wave projects its own rows (row-owner).
+//   kQkvReg: stationary in registers, wave w holding output columns
+//            [w*3D/8, (w+1)*3D/8); the normalized rows of the whole workgroup
+//            are exchanged through LDS and every wave projects all of them.
+enum QkvMode : int { kQkvLds = 1, kQkvReg = 2 };
+
+template <int D, int F, int TM, bool STAGE1, bool QKV, int QMODE>
+struct TailShape {
+  static constexpr int LDD = D + 8;  // row stride of [*, D] tiles (halves)
+  static constexpr int LDF = F + 8;  // row stride of Wout [D, F] (halves)
+  static constexpr int WO = 0;
+  static constexpr int WIN = WO + (STAGE1 ? D * LDD : 0);
+  static constexpr int WOUT = WIN + (STAGE1 ? F * LDD : 0);
+  static constexpr int WQKV = WOUT + (STAGE1 ? D * LDF : 0);
+  static constexpr int NBUF = WQKV + (QKV && QMODE == kQkvLds ? 3 * D * LDD : 0);
+  static constexpr int TOTAL = NBUF + (QKV && QMODE == kQkvReg ? 16 * TM * kTailWaves * LDD : 0);
+  static constexpr int BYTES = TOTAL * 2;
+};
+
+// Copy a [rows, cols] FP16 matrix (row-major, cols % 8 == 0) into LDS with row stride ld.
+__device__ __forceinline__ void stage_matrix(_Float16* dst, const _Float16* src, int rows, int cols, int ld) {
+  const int cpr = cols / 8;
+  for (int c = threadIdx.x; c < rows * cpr; c += kTailThreads) {
+    const int row = c / cpr, col = (c % cpr) * 8;
+    *reinterpret_cast<h8*>(&dst[row * ld + col]) = *reinterpret_cast<const h8*>(&src[(int64_t)row * cols + col]);
+  }
+}
+
+// Row statistics of v (lane holds one row, features 32p + 8g + j; the row is spread over the 4 lane groups).
+template <int PN>
+__device__ __forceinline__ void row_stats(const float (&v)[PN][8], float inv_d, float eps, float& mean, float& rstd) {
+  float sum = 0.f;
+#pragma unroll
+  for (int p = 0; p < PN; ++p)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += v[p][j];
+  mean = sum_over_groups(sum) * inv_d;
+  float sq = 0.f;
+#pragma unroll
+  for (int p = 0; p < PN; ++p)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float c = v[p][j] - mean;
+      sq += c * c;
+    }
+  rstd = rsqrtf(sum_over_groups(sq) * inv_d + eps);
+}
+
+// Per-tile inputs of one wave, prefetched one tile ahead.
+template <int D, int TM, bool STAGE1>
+struct TileIn {
+  h8 ctx[STAGE1 ? TM : 1][D / 32];
+  float x[TM][D / 32][8];
+};
+
+template <int D, int TM, bool STAGE1>
+__device__ __forceinline__ void load_tile(TileIn<D, TM, STAGE1>& in, const TailArgs& a, int64_t m0, int r, int g) {
+  constexpr int PN = D / 32;
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    const int64_t m = m0 + 16 * t + r;
+    const bool valid = m < a.m;
+    if constexpr (STAGE1) {
+#pragma unroll
+      for (int ks = 0; ks < PN; ++ks)
+        in.ctx[t][ks] = valid ? *reinterpret_cast<const h8*>(a.ctx + m * D + ks * 32 + 8 * g) : zero_h8();
+    }
+#pragma unroll
+    for (int p = 0; p < PN; ++p) {
+      if (valid) {
+        load8_f32(a.x + m * D + 32 * p + 8 * g, in.x[t][p]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) in.x[t][p][j] = 0.f;
+      }
+    }
+  }
+}
+
+template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE>
+__global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
+  constexpr bool QKV = !LAST;
+  using SH = TailShape<D, F, TM, STAGE1, QKV, QMODE>;
+  constexpr int PN = D / 32;   // feature pairs of a D-wide row
+  constexpr int KS = D / 32;   // k-steps over D
+  constexpr int FQ = F / 32;   // hidden feature pairs
+  constexpr int QP = 3 * D / 32;
+  constexpr int ROWS = 16 * TM * kTailWaves;
+  constexpr int QNW = 3 * D / kTailWaves;  // QKV columns per wave (register mode)
+  constexpr int QNT = QNW / 16;            // 16-column tiles per wave (register mode)
+  static_assert(D % 32 == 0 && F % 32 == 0, "shape");
+  static_assert(QMODE != kQkvReg || QNT * 16 * kTailWaves == 3 * D, "register mode needs 3D/16 divisible by 8");
+
+  extern __shared__ __align__(16) _Float16 lds[];
+
+  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = l & 15, g = l >> 4;
+
+  if constexpr (STAGE1) {
+    stage_matrix(lds + SH::WO, a.wo, D, D, SH::LDD);
+    stage_matrix(lds + SH::WIN, a.win, F, D, SH::LDD);
+    stage_matrix(lds + SH::WOUT, a.wout, D, F, SH::LDF);
+  }
+  if constexpr (QKV && QMODE == kQkvLds) stage_matrix(lds + SH::WQKV, a.wqkv, 3 * D, D, SH::LDD);
+  h8 wq[QKV && QMODE == kQkvReg ? QNT : 1][KS];
+  if constexpr (QKV && QMODE == kQkvReg) {
+#pragma unroll
+    for (int nt = 0; nt < QNT; ++nt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        wq[nt][ks] = *reinterpret_cast<const h8*>(a.wqkv + (int64_t)(QNW * wave + 16 * nt + r) * D + ks * 32 + 8 * g);
+  }
+  __syncthreads();
+
+  const float inv_d = 1.0f / (float)D;
+  const int64_t M = a.m;
+  const int64_t ntiles = (M + ROWS - 1) / ROWS;
+
+  int64_t tile = blockIdx.x;
+  TileIn<D, TM, STAGE1> cur;
+  load_tile<D, TM, STAGE1>(cur, a, tile * ROWS + wave * 16 * TM, r, g);
+
+  for (; tile < ntiles; tile += gridDim.x) {
+    const int64_t wg0 = tile * ROWS;
+    const int64_t m0 = wg0 + wave * 16 * TM;
+    TileIn<D, TM, STAGE1> nxt;
+    if (tile + gridDim.x < ntiles) load_tile<D, TM, STAGE1>(nxt, a, (tile + gridDim.x) * ROWS + wave * 16 * TM, r, g);
+
+    // xr: the residual stream of this wave's rows (lane holds row m0+16t+r, features 32p+8g+j)
+    float xr[TM][PN][8];
+    if constexpr (STAGE1) {
+      // ---- out-projection + residual + LN2 ----
+      h8 n2f[TM][KS];
+#pragma unroll
+      for (int t = 0; t < TM; ++t) {
+        f4 acc[PN][2];
+#pragma unroll
+        for (int p = 0; p < PN; ++p) acc[p][0] = acc[p][1] = zero4();
+#pragma unroll
+        for (int p = 0; p < PN; ++p) {
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+              const h8 w = *reinterpret_cast<const h8*>(
+                  &lds[SH::WO + (32 * p + pair_row(r, tt)) * SH::LDD + ks * 32 + 8 * g]);
+              acc[p][tt] = mfma32(w, cur.ctx[t][ks], acc[p][tt]);
+            }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int p = 0; p < PN; ++p) {
+          float bv[8];
+          load8_f16_to_f32(a.bo + 32 * p + 8 * g, bv);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            xr[t][p][i] = (acc[p][0][i] + bv[i]) + cur.x[t][p][i];
+            xr[t][p][4 + i] = (acc[p][1][i] + bv[4 + i]) + cur.x[t][p][4 + i];
+          }
+        }
+        float mean, rstd;
+        row_stats<PN>(xr[t], inv_d, a.eps2, mean, rstd);
+#pragma unroll
+        for (int p = 0; p < PN; ++p) {
+          const int n = 32 * p + 8 * g;
+          float gm[8], bt[8];
+          load8_f32(a.g2 + n, gm);
+          load8_f32(a.be2 + n, bt);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) n2f[t][p][j] = (_Float16)((xr[t][p][j] - mean) * rstd * gm[j] + bt[j]);
+        }
+      }
+
+      // ---- FFN: x'' = x' + Wout fp16(GELU(Win n2 + bin)) + bout ----
+      f4 yacc[TM][PN][2];
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int p = 0; p < PN; ++p) yacc[t][p][0] = yacc[t][p][1] = zero4();
+#pragma unroll 1
+      for (int fq = 0; fq < FQ; ++fq) {
+        f4 hacc[TM][2];
+#pragma unroll
+        for (int t = 0; t < TM; ++t) hacc[t][0] = hacc[t][1] = zero4();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            const h8 w = *reinterpret_cast<const h8*>(
+                &lds[SH::WIN + (32 * fq + pair_row(r, tt)) * SH::LDD + ks * 32 + 8 * g]);
+#pragma unroll
+            for (int t = 0; t < TM; ++t) hacc[t][tt] = mfma32(w, n2f[t][ks], hacc[t][tt]);
+          }
+        float bi[8];
+        load8_f16_to_f32(a.bin + 32 * fq + 8 * g, bi);
+        h8 hb[TM];
+#pragma unroll
+        for (int t = 0; t < TM; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            hb[t][i] = (_Float16)gelu_erf(hacc[t][0][i] + bi[i]);
+            hb[t][4 + i] = (_Float16)gelu_erf(hacc[t][1][i] + bi[4 + i]);
+          }
+#pragma unroll
+        for (int p = 0; p < PN; ++p)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            const h8 w = *reinterpret_cast<const h8*>(
+                &lds[SH::WOUT + (32 * p + pair_row(r, tt)) * SH::LDF + 32 * fq + 8 * g]);
+#pragma unroll
+            for (int t = 0; t < TM; ++t) yacc[t][p][tt] = mfma32(w, hb[t], yacc[t][p][tt]);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int t = 0; t < TM; ++t) {
+        const int64_t m = m0 + 16 * t + r;
+#pragma unroll
+        for (int p = 0; p < PN; ++p) {
+          const int n = 32 * p + 8 * g;
+          float bv[8];
+          load8_f16_to_f32(a.bout + n, bv);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            xr[t][p][i] = (yacc[t][p][0][i] + bv[i]) + xr[t][p][i];
+            xr[t][p][4 + i] = (yacc[t][p][1][i] + bv[4 + i]) + xr[t][p][4 + i];
+          }
+          if (m < M) store8(a.x_out + m * D + n, xr[t][p]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int p = 0; p < PN; ++p)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) xr[t][p][j] = cur.x[t][p][j];
+    }
+
+    // ---- next LayerNorm, then the next layer's QKV projection (or the final output) ----
+    h8 n1f[TM][KS];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+      const int64_t m = m0 + 16 * t + r;
+      float mean, rstd;
+      row_stats<PN>(xr[t], inv_d, a.eps1, mean, rstd);
+#pragma unroll
+      for (int p = 0; p < PN; ++p) {
+        const int n = 32 * p + 8 * g;
+        float gm[8], bt[8], o[8];
+        load8_f32(a.g1 + n, gm);
+        load8_f32(a.be1 + n, bt);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = (xr[t][p][j] - mean) * rstd * gm[j] + bt[j];
+        if constexpr (LAST) {
+          if (m < M) store8(static_cast<float*>(a.out) + m * D + n, o);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) n1f[t][p][j] = (_Float16)o[j];
+        }
+      }
+    }
+
+    if constexpr (QKV && QMODE == kQkvLds) {
+      _Float16* qkv = static_cast<_Float16*>(a.out);
+#pragma unroll 1
+      for (int op = 0; op < QP; ++op) {
+        f4 qacc[TM][2];
+#pragma unroll
+        for (int t = 0; t < TM; ++t) qacc[t][0] = qacc[t][1] = zero4();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            const h8 w = *reinterpret_cast<const h8*>(
+                &lds[SH::WQKV + (32 * op + pair_row(r, tt)) * SH::LDD + ks * 32 + 8 * g]);
+#pragma unroll
+            for (int t = 0; t < TM; ++t) qacc[t][tt] = mfma32(w, n1f[t][ks], qacc[t][tt]);
+          }
+        const int n = 32 * op + 8 * g;
+        float bv[8];
+        load8_f16_to_f32(a.bqkv + n, bv);
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+          const int64_t m = m0 + 16 * t + r;
+          float v[8];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[i] = qacc[t][0][i] + bv[i];
+            v[4 + i] = qacc[t][1][i] + bv[4 + i];
+          }
+          if (m < M) store8(qkv + m * (3 * D) + n, v);
+        }
+      }
+    }
+
+    if constexpr (QKV && QMODE == kQkvReg) {
+      // publish this wave's normalized rows, then project all workgroup rows onto this wave's columns
+      _Float16* nbuf = lds + SH::NBUF;
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int p = 0; p < PN; ++p)
+          *reinterpret_cast<h8*>(&nbuf[(wave * 16 * TM + 16 * t + r) * SH::LDD + 32 * p + 8 * g]) = n1f[t][p];
+      __syncthreads();
+      _Float16* qkv = static_cast<_Float16*>(a.out);
+      const int ncol0 = QNW * wave;
+      float bq[QNT][4];
+#pragma unroll
+      for (int nt = 0; nt < QNT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bq[nt][i] = (float)a.bqkv[ncol0 + 16 * nt + 4 * g + i];
+#pragma unroll 2
+      for (int mt = 0; mt < ROWS / 16; ++mt) {
+        h8 bn[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          bn[ks] = *reinterpret_cast<const h8*>(&nbuf[(16 * mt + r) * SH::LDD + ks * 32 + 8 * g]);
+        const int64_t m = wg0 + 16 * mt + r;
+#pragma unroll
+        for (int nt = 0; nt < QNT; ++nt) {
+          f4 acc = zero4();
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) acc = mfma32(wq[nt][ks], bn[ks], acc);
+          if (m < M) {
+            h4 o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = (_Float16)(acc[i] + bq[nt][i]);
+            *reinterpret_cast<h4*>(qkv + m * (3 * D) + ncol0 + 16 * nt + 4 * g) = o;
+          }
+        }
+      }
+      __syncthreads();  // nbuf is rewritten by the next tile
+    }
+    cur = nxt;
+  }
+}
+
+static int tail_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE>
+static hipError_t launch_tail(const TailArgs& a, hipStream_t s) {
+  using SH = TailShape<D, F, TM, STAGE1, !LAST, QMODE>;
+  constexpr int lds_bytes = SH::BYTES;
+  static_assert(lds_bytes <= kLdsBudget, "weights exceed LDS");
+  auto kern = layer_tail_kernel<D, F, TM, STAGE1, LAST, QMODE>;
+  if (lds_bytes > 64 * 1024) {
+    static std::atomic<bool> attribute_set{false};  // once per instantiation
+    if (!attribute_set.load(std::memory_order_acquire)) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
+      if (e != hipSuccess) return e;
+      attribute_set.store(true, std::memory_order_release);
+    }
+  }
+  constexpr int ROWS = 16 * TM * kTailWaves;
+  const int64_t ntiles = (a.m + ROWS - 1) / ROWS;
+  const int64_t per_cu = lds_bytes > kLdsBudget / 2 ? 1 : 2;
+  int64_t grid = (int64_t)tail_cu_count() * per_cu;
+  if (grid > ntiles) grid = ntiles;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kTailThreads), lds_bytes, s, a);
+  return hipGetLastError();
+}
+
+// QKV weights in LDS when the whole set fits, else stationary in registers.
+template <int D, int F, bool STAGE1>
+constexpr int qkv_mode() {
+  return TailShape<D, F, 1, STAGE1, true, kQkvLds>::BYTES <= kLdsBudget ? kQkvLds : kQkvReg;
+}
+
+template <int D, int F, bool STAGE1>
+static hipError_t tail_variant(int variant, bool last, const TailArgs& a, hipStream_t s) {
+  constexpr int QM = qkv_mode<D, F, STAGE1>();
+  // variant 2 (32 rows per wave) only where its LDS footprint still fits
+  if constexpr (TailShape<D, F, 2, STAGE1, true, QM>::BYTES <= kLdsBudget) {
+    if (variant == 2)
+      return last ? launch_tail<D, F, 2, STAGE1, true, QM>(a, s) : launch_tail<D, F, 2, STAGE1, false, QM>(a, s);
+  }
+  return last ? launch_tail<D, F, 1, STAGE1, true, QM>(a, s) : launch_tail<D, F, 1, STAGE1, false, QM>(a, s);
+}
+
+}  // namespace mpk
+
+using namespace mpk;
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+extern "C" int mpk_layer_tail_supported(int32_t d, int32_t f) {
+  return (d == 32 && f == 64) || (d == 64 && (f == 64 || f == 128 || f == 256)) ||
+         (d == 128 && f == 128) || (d == 32 && f == 32) || (d == 32 && f == 128);
+}
+
+extern "C" int mpk_layer_tail(const void* ctx, const float* x, const void* w_o, const void* b_o, const float* ln2_w,
+                              const float* ln2_b, const void* w_in, const void* b_in, const void* w_out,
+                              const void* b_out, const float* next_ln_w, const float* next_ln_b, const void* w_qkv,
+                              const void* b_qkv, float* x_out, void* out, int last, int64_t m, int32_t d, int32_t f,
+                              float ln2_eps, float next_ln_eps, int variant, void* stream) {
+  if (!ctx || !x || !w_o || !b_o || !ln2_w || !ln2_b || !w_in || !b_in || !w_out || !b_out || !next_ln_w ||
+      !next_ln_b || !x_out || !out || m < 0)
+    return MPK_EINVAL;
+  if (!last && (!w_qkv || !b_qkv)) return MPK_EINVAL;
+  if (!mpk_layer_tail_supported(d, f)) return MPK_EUNSUPPORTED;
+  const void* ptrs[] = {ctx, x, w_o, b_o, ln2_w, ln2_b, w_in, b_in, w_out, b_out, next_ln_w, next_ln_b, x_out, out};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return MPK_EALIGN;
+  if (!last && (!aligned16(w_qkv) || !aligned16(b_qkv))) return MPK_EALIGN;
+  if (m == 0) return MPK_OK;
+  if (variant == 0) variant = 1;
+  if (variant != 1 && variant != 2) return MPK_EUNSUPPORTED;
+  TailArgs a{};
+  a.ctx = static_cast<const _Float16*>(ctx); a.x = x;
+  a.wo = static_cast<const _Float16*>(w_o); a.bo = static_cast<const _Float16*>(b_o); a.g2 = ln2_w; a.be2 = ln2_b;
+  a.win = static_cast<const _Float16*>(w_in); a.bin = static_cast<const _Float16*>(b_in);
+  a.wout = static_cast<const _Float16*>(w_out); a.bout = static_cast<const _Float16*>(b_out);
+  a.g1 = next_ln_w; a.be1 = next_ln_b;
+  a.wqkv = static_cast<const _Float16*>(w_qkv); a.bqkv = static_cast<const _Float16*>(b_qkv);
+  a.x_out = x_out; a.out = out; a.m = m; a.f = f; a.eps2 = ln2_eps; a.eps1 = next_ln_eps;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool L = last != 0;
+  hipError_t e;
+  if (d == 32 && f == 32) e = tail_variant<32, 32, true>(variant, L, a, s);
+  else if (d == 32 && f == 64) e = tail_variant<32, 64, true>(variant, L, a, s);
+  else if (d == 32 && f == 128) e = tail_variant<32, 128, true>(variant, L, a, s);
+  else if (d == 64 && f == 64) e = tail_variant<64, 64, true>(variant, L, a, s);
+  else if (d == 64 && f == 128) e = tail_variant<64, 128, true>(variant, L, a, s);
+  else if (d == 64 && f == 256) e = tail_variant<64, 256, true>(variant, L, a, s);
+  else e = tail_variant<128, 128, true>(variant, L, a, s);
+  return (int)e;
+}
+
+extern "C" int mpk_layernorm_qkv_supported(int32_t d) { return d == 32 || d == 64 || d == 128; }
+
+extern "C" int mpk_layernorm_qkv(const float* x, const float* ln_w, const float* ln_b, const void* w_qkv,
+                                 const void* b_qkv, void* qkv, int64_t m, int32_t d, float eps, int variant,
+                                 void* stream) {
+  if (!x || !ln_w || !ln_b || !w_qkv || !b_qkv || !qkv || m < 0) return MPK_EINVAL;
+  if (!mpk_layernorm_qkv_supported(d)) return MPK_EUNSUPPORTED;
+  const void* ptrs[] = {x, ln_w, ln_b, w_qkv, b_qkv, qkv};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return MPK_EALIGN;
+  if (m == 0) return MPK_OK;
+  if (variant == 0) variant = 1;
+  if (variant != 1 && variant != 2) return MPK_EUNSUPPORTED;
+  TailArgs a{};
+  a.x = x; a.g1 = ln_w; a.be1 = ln_b;
+  a.wqkv = static_cast<const _Float16*>(w_qkv); a.bqkv = static_cast<const _Float16*>(b_qkv);
+  a.out = qkv; a.m = m; a.eps1 = eps;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (d) {
+    case 32: e = tail_variant<32, 32, false>(variant, false, a, s); break;
+    case 64: e = tail_variant<64, 32, false>(variant, false, a, s); break;
+    default: e = tail_variant<128, 32, false>(variant, false, a, s); break;
+  }
+  return (int)e;
+}

@@ -23,64 +23,74 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-template <int G, int NV, bool HAS_U, typename OT>
+template <int G, int NV, int R, bool HAS_U, typename OT>
 __global__ __launch_bounds__(kBlock) void residual_layernorm_kernel(
     const float* __restrict__ x, const float* __restrict__ u, const float* __restrict__ gamma,
     const float* __restrict__ beta, float* __restrict__ res_out, OT* __restrict__ norm_out, int64_t rows,
     int d, float eps) {
+  constexpr int GPB = kBlock / G;  // row groups per block
   const int lane = threadIdx.x % G;
-  const int64_t row = (int64_t)blockIdx.x * (kBlock / G) + threadIdx.x / G;
-  if (row >= rows) return;  // a whole group leaves together; shuffles stay inside the group
+  const int64_t base = (int64_t)blockIdx.x * GPB * R + threadIdx.x / G;
   const int nvec = d >> 2;
-  const float* xr = x + row * d;
-  float4 r[NV];
-  float sum = 0.f;
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int c = lane + v * G;
-    if (c < nvec) {
-      float4 a = reinterpret_cast<const float4*>(xr)[c];
-      if (HAS_U) {
-        const float4 b = reinterpret_cast<const float4*>(u + row * d)[c];
-        a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
-      }
-      r[v] = a;
-      sum += (a.x + a.y) + (a.z + a.w);
-    } else {
-      r[v] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  }
   const float inv_d = 1.0f / (float)d;
-  const float mean = group_sum<G>(sum) * inv_d;
-  float sq = 0.f;
+
+  // Issue every load of the R rows first (more bytes in flight per lane).
+  float4 r[R][NV];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int c = lane + v * G;
-    if (c < nvec) {
-      const float a = r[v].x - mean, b = r[v].y - mean, e = r[v].z - mean, f = r[v].w - mean;
-      sq += (a * a + b * b) + (e * e + f * f);
+  for (int k = 0; k < R; ++k) {
+    const int64_t row = base + (int64_t)k * GPB;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int c = lane + v * G;
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (row < rows && c < nvec) {
+        a = reinterpret_cast<const float4*>(x + row * d)[c];
+        if (HAS_U) {
+          const float4 b = reinterpret_cast<const float4*>(u + row * d)[c];
+          a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+        }
+      }
+      r[k][v] = a;
     }
   }
-  const float rstd = rsqrtf(group_sum<G>(sq) * inv_d + eps);
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int c = lane + v * G;
-    if (c < nvec) {
-      if (HAS_U) reinterpret_cast<float4*>(res_out + row * d)[c] = r[v];
-      const float4 gm = reinterpret_cast<const float4*>(gamma)[c];
-      const float4 bt = reinterpret_cast<const float4*>(beta)[c];
-      float o[4];
-      o[0] = (r[v].x - mean) * rstd * gm.x + bt.x;
-      o[1] = (r[v].y - mean) * rstd * gm.y + bt.y;
-      o[2] = (r[v].z - mean) * rstd * gm.z + bt.z;
-      o[3] = (r[v].w - mean) * rstd * gm.w + bt.w;
-      OT* dst = norm_out + row * d + 4 * c;
-      if constexpr (sizeof(OT) == 4) {
-        *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
-      } else {
-        h4 h;
-        h[0] = (_Float16)o[0]; h[1] = (_Float16)o[1]; h[2] = (_Float16)o[2]; h[3] = (_Float16)o[3];
-        *reinterpret_cast<h4*>(dst) = h;
+  for (int k = 0; k < R; ++k) {
+    const int64_t row = base + (int64_t)k * GPB;
+    float sum = 0.f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) sum += (r[k][v].x + r[k][v].y) + (r[k][v].z + r[k][v].w);
+    const float mean = group_sum<G>(sum) * inv_d;
+    float sq = 0.f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int c = lane + v * G;
+      if (c < nvec) {
+        const float a = r[k][v].x - mean, b = r[k][v].y - mean, e = r[k][v].z - mean, f = r[k][v].w - mean;
+        sq += (a * a + b * b) + (e * e + f * f);
+      }
+    }
+    const float rstd = rsqrtf(group_sum<G>(sq) * inv_d + eps);
+    if (row >= rows) continue;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int c = lane + v * G;
+      if (c < nvec) {
+        if (HAS_U) reinterpret_cast<float4*>(res_out + row * d)[c] = r[k][v];
+        const float4 gm = reinterpret_cast<const float4*>(gamma)[c];
+        const float4 bt = reinterpret_cast<const float4*>(beta)[c];
+        float o[4];
+        o[0] = (r[k][v].x - mean) * rstd * gm.x + bt.x;
+        o[1] = (r[k][v].y - mean) * rstd * gm.y + bt.y;
+        o[2] = (r[k][v].z - mean) * rstd * gm.z + bt.z;
+        o[3] = (r[k][v].w - mean) * rstd * gm.w + bt.w;
+        OT* dst = norm_out + row * d + 4 * c;
+        if constexpr (sizeof(OT) == 4) {
+          *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+          h4 h;
+          h[0] = (_Float16)o[0]; h[1] = (_Float16)o[1]; h[2] = (_Float16)o[2]; h[3] = (_Float16)o[3];
+          *reinterpret_cast<h4*>(dst) = h;
+        }
       }
     }
   }
@@ -89,10 +99,12 @@ __global__ __launch_bounds__(kBlock) void residual_layernorm_kernel(
 template <int G, int NV, bool HAS_U, typename OT>
 static hipError_t launch_ln(const float* x, const float* u, const float* gamma, const float* beta,
                             float* res_out, OT* norm_out, int64_t rows, int d, float eps, hipStream_t s) {
-  const int64_t rows_per_block = kBlock / G;
+  constexpr int R = NV >= 4 ? 1 : 4 / NV;  // rows per group: ~64 bytes of x in flight per lane
+  const int64_t rows_per_block = (kBlock / G) * R;
   const int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL((residual_layernorm_kernel<G, NV, HAS_U, OT>), dim3((unsigned)blocks), dim3(kBlock), 0, s, x,
-                     u, gamma, beta, res_out, norm_out, rows, d, eps);
+  if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((residual_layernorm_kernel<G, NV, R, HAS_U, OT>), dim3((unsigned)blocks), dim3(kBlock), 0, s,
+                     x, u, gamma, beta, res_out, norm_out, rows, d, eps);
   return hipGetLastError();
 }
 

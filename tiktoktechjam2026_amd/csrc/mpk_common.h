@@ -5,8 +5,8 @@
 // * Wavefronts are 64 lanes.  A lane index l splits as r = l % 16 (MFMA row/col)
 //   and g = l / 16 (the lane group that owns a k-slice of an MFMA operand).
 // * All matrix products use v_mfma_f32_16x16x32_f16 (FP16 x FP16 -> FP32) or, for
-//   16-wide head dims, v_mfma_f32_16x16x16_f16.  Operand layouts (checked on the
-//   device by tests/test_kernels_gpu.py::test_mfma_lane_layout):
+//   16-wide head dims, v_mfma_f32_16x16x16_f16.  Operand layouts (every GEMM and
+//   attention parity test in tests/test_kernels_gpu.py depends on them):
 //     A (16 x K): lane l holds row r, k = 8g .. 8g+7          (16x16x32)
 //     B (K x 16): lane l holds col r, k = 8g .. 8g+7
 //     C (16 x 16): lane l holds col r, rows 4g .. 4g+3
@@ -99,17 +99,24 @@ __device__ __forceinline__ void store8(_Float16* p, const float* v) {
 // Exact (erf-based) GELU in FP32: 0.5 v (1 + erf(v / sqrt(2))).
 __device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
 
-// Sum over the four lane groups g that share one MFMA column (lanes l, l^16, l^32, l^48).
+// Reductions over the four lane groups g that share one MFMA column (lanes l,
+// l^16, l^32, l^48), with the gfx950 row-swap instructions: permlane16_swap
+// exchanges rows 1/3 of one operand with rows 0/2 of the other and
+// permlane32_swap the upper and lower 32-lane halves, so calling them with the
+// same value twice yields (own, partner) pairs in every lane.  Both partners
+// evaluate the same commutative expression, so all four lanes end bit-identical.
 __device__ __forceinline__ float sum_over_groups(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 __device__ __forceinline__ float max_over_groups(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // Map a linear workgroup id so that consecutive tile indices land on the same

@@ -13,11 +13,16 @@ the shape is only
   library's built-in table (``mpk_*_auto_variant``); entries in ``TUNED``
   override it for shapes measured on MI355X (256 CUs, 64-lane waves).
 
+When the whole layer tail fits one kernel (``LAYER_TAIL_SHAPES``) the forward
+runs 1 + 2L launches: LayerNorm+QKV, then per layer attention and the fused
+tail (out-proj+LN2+FFN+LN1'+QKV', or the final LayerNorm on the last layer).
+
 Tile variants (see the kernel sources for the exact tiles):
   qkv / ffn-in projection  1: 128x128 (2x2 waves)  2: 128x64  3: 128x32  4: 64x128
   out-proj + LN            1: 64 rows/WG           2: 128 rows/WG (d <= 128)
   fused FFN + LN           1: 16 rows/wave         2: 32 rows/wave (d <= 256)
   attention                1: 16 queries/wave      2: 32 queries/wave (hd <= 64)
+  layer tail / LN+QKV      1: 16 rows/wave         2: 32 rows/wave
 """
 
 from __future__ import annotations
@@ -29,6 +34,10 @@ import torch
 
 LN_FUSED_WIDTHS = (32, 64, 128, 256, 512)
 ATTENTION_HEAD_DIMS = (16, 32, 64, 128)
+# (d_model, ffn_dim) pairs built into the whole-layer tail kernel (its weights fit in LDS);
+# must equal mpk_layer_tail_supported / mpk_layernorm_qkv_supported in the library.
+LAYER_TAIL_SHAPES = frozenset({(32, 32), (32, 64), (32, 128), (64, 64), (64, 128), (64, 256), (128, 128)})
+LAYERNORM_QKV_WIDTHS = frozenset({32, 64, 128})
 
 
 @dataclass(frozen=True)
@@ -41,12 +50,15 @@ class Route:
     fp16_attention: bool = True
     fuse_attention_output_norm: bool = True
     fuse_full_ffn: bool = True
+    fuse_layer_tail: bool = False
     qkv_variant: int = 0
     attention_variant: int = 0
     out_ln_variant: int = 0
     ffn_variant: int = 0
     ffn_in_variant: int = 0
     ffn_out_variant: int = 0
+    tail_variant: int = 0
+    head_variant: int = 0
     notes: Tuple[str, ...] = field(default_factory=tuple)
 
     def describe(self) -> Dict[str, object]:
@@ -57,6 +69,7 @@ class Route:
             "attention": "hip_fp16_flash" if self.fp16_attention else "hip_fp32io_flash",
             "attention_output_norm_fusion": self.fuse_attention_output_norm,
             "full_ffn_fusion": self.fuse_full_ffn,
+            "layer_tail_fusion": self.fuse_layer_tail,
             "variants": {
                 "qkv": self.qkv_variant,
                 "attention": self.attention_variant,
@@ -64,6 +77,8 @@ class Route:
                 "ffn": self.ffn_variant,
                 "ffn_in": self.ffn_in_variant,
                 "ffn_out": self.ffn_out_variant,
+                "layer_tail": self.tail_variant,
+                "layernorm_qkv": self.head_variant,
             },
         }
 
@@ -103,6 +118,12 @@ def plan(
         return Route(False, "d_model above 2048")
     fuse_out = enable_attention_output_norm_fusion and d in LN_FUSED_WIDTHS
     fuse_ffn = enable_full_ffn_fusion and d in LN_FUSED_WIDTHS and f % 32 == 0
+    # The layer-tail kernel chains out-proj+LN2 -> FFN+LN -> next QKV; it needs both
+    # fusions, the FP16 normalized stream and FP16 attention I/O.
+    fuse_tail = (
+        fuse_out and fuse_ffn and enable_fp16_normalized_stream and enable_fp16_custom_attention
+        and (d, f) in LAYER_TAIL_SHAPES and d in LAYERNORM_QKV_WIDTHS
+    )
     route = Route(
         True,
         "hip",
@@ -110,6 +131,7 @@ def plan(
         fp16_attention=enable_fp16_custom_attention,
         fuse_attention_output_norm=fuse_out,
         fuse_full_ffn=fuse_ffn,
+        fuse_layer_tail=fuse_tail,
     )
     tuned = TUNED.get((d, f, h, _token_bucket(int(config.batch_size) * int(config.seq_len))))
     if tuned:

@@ -34,6 +34,7 @@ import torch.nn as nn
 
 from .. import dispatch
 from ..custom_kernel.hip_attention import attention
+from .hip_fused import fused_layer_tail, layer_norm_qkv
 from .hip_linear import (
     layer_norm,
     mixed_add_layer_norm,
@@ -67,12 +68,16 @@ class MixedPrecisionSelfAttention(nn.Module):
         causal: bool,
     ) -> torch.Tensor:
         """QKV projection + flash attention -> context ``[B, S, D]`` (fp16, or fp32 on the fp32-I/O route)."""
-        batch, seq_len, _ = normalized.shape
         route = self.route
         qkv_dtype = torch.float16 if route.fp16_attention else torch.float32
         qkv = mixed_linear(normalized, self.qkv_proj, output_dtype=qkv_dtype, variant=route.qkv_variant)
+        return self.attend(qkv, key_valid, causal)
+
+    def attend(self, qkv: torch.Tensor, key_valid: Optional[torch.Tensor], causal: bool) -> torch.Tensor:
+        """Flash attention over a packed ``[B, S, 3D]`` projection -> context ``[B, S, D]``."""
+        batch, seq_len, _ = qkv.shape
         q, k, v = qkv.view(batch, seq_len, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
-        ctx = attention(q, k, v, self.scale, causal=causal, key_valid=key_valid, variant=route.attention_variant)
+        ctx = attention(q, k, v, self.scale, causal=causal, key_valid=key_valid, variant=self.route.attention_variant)
         return ctx.view(batch, seq_len, self.d_model)
 
     def forward(
@@ -189,6 +194,11 @@ class MixedPrecisionTransformer(nn.Module):
     def dispatch_report(self) -> Dict[str, object]:
         return self.route.describe()
 
+    def _forward_layer_tail(self, x: torch.Tensor, key_valid: Optional[torch.Tensor], causal: bool,
+                            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """1 + 2L launches: LayerNorm+QKV, then per layer attention and the fused layer tail."""
+        return _forward_layer_tail_impl(self, x, key_valid, causal, out)
+
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         if x.dtype != torch.float32:
             raise ValueError("mixed candidate requires an FP32 input/residual stream")
@@ -198,6 +208,12 @@ class MixedPrecisionTransformer(nn.Module):
         causal = bool(self.config.causal)
         stream_dtype = self.route.normalized_dtype
         n_layers = len(self.layers)
+
+        if self.route.fuse_layer_tail:
+            normalized = self._forward_layer_tail(x, effective_mask, causal)
+            if effective_mask is not None:
+                return normalized.masked_fill(~effective_mask[..., None], 0)
+            return normalized
 
         normalized = layer_norm(x, self.layers[0].norm1, normalized_dtype=stream_dtype)
         for index, layer in enumerate(self.layers):
@@ -211,6 +227,29 @@ class MixedPrecisionTransformer(nn.Module):
         if effective_mask is not None:
             return normalized.masked_fill(~effective_mask[..., None], 0)
         return normalized
+
+
+def _forward_layer_tail_impl(model: "MixedPrecisionTransformer", x, key_valid, causal, out=None):
+    route = model.route
+    layers = model.layers
+    qkv = layer_norm_qkv(x, layers[0].norm1, layers[0].attention.qkv_proj, variant=route.head_variant)
+    result = None
+    for index, layer in enumerate(layers):
+        att = layer.attention
+        ctx = att.attend(qkv, key_valid, causal)
+        last = index + 1 == len(layers)
+        if last:
+            x, result = fused_layer_tail(
+                ctx, x, att.out_proj, layer.norm2, layer.ffn_in, layer.ffn_out, model.final_norm, None,
+                variant=route.tail_variant, out=out,
+            )
+        else:
+            nxt = layers[index + 1]
+            x, qkv = fused_layer_tail(
+                ctx, x, att.out_proj, layer.norm2, layer.ffn_in, layer.ffn_out, nxt.norm1, nxt.attention.qkv_proj,
+                variant=route.tail_variant,
+            )
+    return result
 
 
 def _source_state(baseline: Union[nn.Module, Mapping[str, torch.Tensor]]) -> Dict[str, torch.Tensor]:

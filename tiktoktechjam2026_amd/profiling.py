@@ -1,8 +1,9 @@
 """Per-kernel timing and roofline accounting for the HIP forward.
 
 ``forward_kernel_table`` times every distinct kernel launch of one forward
-(initial LayerNorm, QKV projection, attention, out-projection + LN, FFN + LN)
-in isolation with HIP events recorded on the stream the kernel is launched on
+(per-operator route: initial LayerNorm, QKV projection, attention,
+out-projection + LN, FFN + LN; fused route: LayerNorm + QKV, attention, layer
+tail, last-layer tail) in isolation with HIP events recorded on the stream the kernel is launched on
 (torch's current stream, which is the stream the C ABI is given), and prices
 each against its algorithmic work:
 
@@ -11,6 +12,9 @@ each against its algorithmic work:
 * FFN + residual + LN:            FLOPs 4 M D F; bytes M D s_in + 4 D F + M D (8 + s_norm)
 * causal attention:               FLOPs 2 B H hd S (S+1); bytes 8 B S D (fp16 q, k, v in, o out)
 * LayerNorm (no residual):        bytes M D (4 + s_norm)
+* LayerNorm + QKV:                FLOPs 6 M D^2; bytes 4 M D + 6 M D + 6 D^2
+* layer tail (to the next QKV):   FLOPs 8 M D^2 + 4 M D F; bytes M D (2 + 4 + 4 + 6) + 2 (4 D^2 + 2 D F)
+* last-layer tail (final LN out): FLOPs 2 M D^2 + 4 M D F; bytes 14 M D + 2 (D^2 + 2 D F)
 
 (s_* = bytes per element).  The binding roof of a kernel is the larger of
 FLOPs / MFMA peak and bytes / HBM peak; ``frac`` is achieved / peak on that roof.
@@ -41,7 +45,7 @@ class KernelCost:
         return "mfma" if self.flops / PEAK_FP16_MFMA_FLOPS >= self.bytes / PEAK_HBM_BYTES else "hbm"
 
 
-def forward_costs(config, normalized_bytes: int = 2) -> Dict[str, KernelCost]:
+def forward_costs(config, normalized_bytes: int = 2, fused_tail: bool = False) -> Dict[str, KernelCost]:
     """Algorithmic FLOPs / bytes per launch of each kernel of one forward (one microbatch)."""
     B, S, D = int(config.batch_size), int(config.seq_len), int(config.d_model)
     H, F, L = int(config.num_heads), int(config.ffn_dim), int(config.num_layers)
@@ -49,10 +53,27 @@ def forward_costs(config, normalized_bytes: int = 2) -> Dict[str, KernelCost]:
     hd = D // H
     sn = normalized_bytes
     pairs = S * (S + 1) / 2 if config.causal else S * S
+    attention = KernelCost("attention", L, 4.0 * B * H * hd * pairs, 8.0 * B * S * D)
+    if fused_tail:
+        w_tail = 2.0 * (D * D + 2 * D * F + 3 * D * D)
+        return {
+            "layernorm_qkv": KernelCost(
+                "layernorm_qkv", 1, 2.0 * M * 3 * D * D, M * D * 4 + M * 3 * D * 2 + 2.0 * 3 * D * D
+            ),
+            "attention": attention,
+            "layer_tail": KernelCost(
+                "layer_tail", L - 1, 2.0 * M * D * D + 4.0 * M * D * F + 6.0 * M * D * D,
+                M * D * (2 + 4 + 4) + M * 3 * D * 2 + w_tail,
+            ),
+            "layer_tail_last": KernelCost(
+                "layer_tail_last", 1, 2.0 * M * D * D + 4.0 * M * D * F,
+                M * D * (2 + 4 + 4 + 4) + 2.0 * (D * D + 2 * D * F),
+            ),
+        }
     return {
         "layernorm": KernelCost("layernorm", 1, 0.0, M * D * (4 + sn)),
         "qkv_proj": KernelCost("qkv_proj", L, 2.0 * M * 3 * D * D, M * D * sn + 3 * D * D * 2 + 3 * D * 2 + M * 3 * D * 2),
-        "attention": KernelCost("attention", L, 4.0 * B * H * hd * pairs, 8.0 * B * S * D),
+        "attention": attention,
         "out_proj_ln": KernelCost(
             "out_proj_ln", L, 2.0 * M * D * D, M * D * 2 + 2 * D * D + 8 * M * D + M * D * sn + 16 * D
         ),
@@ -61,24 +82,59 @@ def forward_costs(config, normalized_bytes: int = 2) -> Dict[str, KernelCost]:
 
 
 def time_launches(fn: Callable[[], object], iterations: int, warmup: int = 3) -> float:
-    """Average duration (seconds) of ``fn`` launches, HIP events on the current stream."""
+    """Average device duration (seconds) of one ``fn`` launch.
+
+    ``iterations`` launches are captured into one HIP graph (so host launch
+    overhead cannot hide in the figure) and the graph replay is bracketed by
+    HIP events on the current stream - the stream the C ABI launches on.
+    """
     for _ in range(warmup):
         fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iterations):
+            fn()
+    graph.replay()  # warm the captured sequence once
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
-    for _ in range(iterations):
-        fn()
+    graph.replay()
     end.record(stream)
     end.synchronize()
-    return start.elapsed_time(end) / 1e3 / iterations
+    seconds = start.elapsed_time(end) / 1e3 / iterations
+    del graph
+    return seconds
+
+
+def _row(name: str, cost: KernelCost, seconds: float) -> Dict[str, object]:
+    if cost.bound == "mfma":
+        achieved, peak, unit = cost.flops / seconds / 1e12, PEAK_FP16_MFMA_FLOPS / 1e12, "TFLOP/s"
+    else:
+        achieved, peak, unit = cost.bytes / seconds / 1e9, PEAK_HBM_BYTES / 1e9, "GB/s"
+    return {
+        "kernel": name,
+        "launches_per_forward": cost.launches_per_forward,
+        "avg_us": seconds * 1e6,
+        "share_us_per_forward": seconds * 1e6 * cost.launches_per_forward,
+        "bound": cost.bound,
+        "achieved": achieved,
+        "peak": peak,
+        "unit": unit,
+        "frac": achieved / peak,
+        "flops": cost.flops,
+        "bytes": cost.bytes,
+        "tflops": cost.flops / seconds / 1e12,
+        "gbps": cost.bytes / seconds / 1e9,
+    }
 
 
 def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[Dict[str, object]]:
     """Time each distinct kernel of ``model``'s forward on input ``x`` (first layer's weights)."""
     from .custom_kernel.hip_attention import attention
+    from .mixed_precision.hip_fused import fused_layer_tail, layer_norm_qkv
     from .mixed_precision.hip_linear import layer_norm, mixed_ffn_add_layer_norm, mixed_linear, mixed_linear_add_layer_norm
 
     config = model.config
@@ -87,57 +143,51 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
     att = layer.attention
     B, S, D = x.shape
     sdt = route.normalized_dtype
-    costs = forward_costs(config, 2 if sdt == torch.float16 else 4)
+    causal = bool(config.causal)
+    costs = forward_costs(config, 2 if sdt == torch.float16 else 4, route.fuse_layer_tail)
     with torch.inference_mode():
-        normalized = layer_norm(x, layer.norm1, normalized_dtype=sdt)
-        qkv = mixed_linear(normalized, att.qkv_proj, output_dtype=torch.float16, variant=route.qkv_variant)
-        q, k, v = qkv.view(B, S, 3, att.num_heads, att.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
-        ctx = attention(q, k, v, att.scale, causal=bool(config.causal), variant=route.attention_variant).view(B, S, D)
-        resid, nffn = mixed_linear_add_layer_norm(ctx, att.out_proj, x, layer.norm2, normalized_dtype=sdt,
-                                                  variant=route.out_ln_variant)
-        launches = {
-            "layernorm": lambda: layer_norm(x, layer.norm1, normalized_dtype=sdt),
-            "qkv_proj": lambda: mixed_linear(normalized, att.qkv_proj, output_dtype=torch.float16,
-                                             variant=route.qkv_variant),
-            "attention": lambda: attention(q, k, v, att.scale, causal=bool(config.causal),
-                                           variant=route.attention_variant),
-            "out_proj_ln": lambda: mixed_linear_add_layer_norm(ctx, att.out_proj, x, layer.norm2,
-                                                               normalized_dtype=sdt, variant=route.out_ln_variant),
-            "ffn_ln": lambda: mixed_ffn_add_layer_norm(nffn, layer.ffn_in, layer.ffn_out, resid, layer.norm1,
-                                                       normalized_dtype=sdt, variant=route.ffn_variant),
-        }
+        if route.fuse_layer_tail:
+            qkv = layer_norm_qkv(x, layer.norm1, att.qkv_proj, variant=route.head_variant)
+            q, k, v = qkv.view(B, S, 3, att.num_heads, att.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
+            ctx = attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant).view(B, S, D)
+            launches = {
+                "layernorm_qkv": lambda: layer_norm_qkv(x, layer.norm1, att.qkv_proj, variant=route.head_variant),
+                "attention": lambda: attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant),
+                "layer_tail": lambda: fused_layer_tail(ctx, x, att.out_proj, layer.norm2, layer.ffn_in, layer.ffn_out,
+                                                       layer.norm1, att.qkv_proj, variant=route.tail_variant),
+                "layer_tail_last": lambda: fused_layer_tail(ctx, x, att.out_proj, layer.norm2, layer.ffn_in,
+                                                            layer.ffn_out, model.final_norm, None,
+                                                            variant=route.tail_variant),
+            }
+        else:
+            normalized = layer_norm(x, layer.norm1, normalized_dtype=sdt)
+            qkv = mixed_linear(normalized, att.qkv_proj, output_dtype=torch.float16, variant=route.qkv_variant)
+            q, k, v = qkv.view(B, S, 3, att.num_heads, att.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
+            ctx = attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant).view(B, S, D)
+            resid, nffn = mixed_linear_add_layer_norm(ctx, att.out_proj, x, layer.norm2, normalized_dtype=sdt,
+                                                      variant=route.out_ln_variant)
+            launches = {
+                "layernorm": lambda: layer_norm(x, layer.norm1, normalized_dtype=sdt),
+                "qkv_proj": lambda: mixed_linear(normalized, att.qkv_proj, output_dtype=torch.float16,
+                                                 variant=route.qkv_variant),
+                "attention": lambda: attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant),
+                "out_proj_ln": lambda: mixed_linear_add_layer_norm(ctx, att.out_proj, x, layer.norm2,
+                                                                   normalized_dtype=sdt, variant=route.out_ln_variant),
+                "ffn_ln": lambda: mixed_ffn_add_layer_norm(nffn, layer.ffn_in, layer.ffn_out, resid, layer.norm1,
+                                                           normalized_dtype=sdt, variant=route.ffn_variant),
+            }
         rows = []
         for name, fn in launches.items():
-            seconds = time_launches(fn, iterations)
-            cost = costs[name]
-            if cost.bound == "mfma":
-                achieved, peak, unit = cost.flops / seconds / 1e12, PEAK_FP16_MFMA_FLOPS / 1e12, "TFLOP/s"
-            else:
-                achieved, peak, unit = cost.bytes / seconds / 1e9, PEAK_HBM_BYTES / 1e9, "GB/s"
-            rows.append(
-                {
-                    "kernel": name,
-                    "launches_per_forward": cost.launches_per_forward,
-                    "avg_us": seconds * 1e6,
-                    "share_us_per_forward": seconds * 1e6 * cost.launches_per_forward,
-                    "bound": cost.bound,
-                    "achieved": achieved,
-                    "peak": peak,
-                    "unit": unit,
-                    "frac": achieved / peak,
-                    "flops": cost.flops,
-                    "bytes": cost.bytes,
-                    "tflops": cost.flops / seconds / 1e12,
-                    "gbps": cost.bytes / seconds / 1e9,
-                }
-            )
+            if costs[name].launches_per_forward == 0:
+                continue
+            rows.append(_row(name, costs[name], time_launches(fn, iterations)))
     return rows
 
 
-def forward_roofline_seconds(config, microbatches: int = 1) -> float:
+def forward_roofline_seconds(config, microbatches: int = 1, fused_tail: bool = False) -> float:
     """Lower bound on one forward: sum over kernels of max(FLOPs/MFMA peak, bytes/HBM peak)."""
     total = 0.0
-    for cost in forward_costs(config).values():
+    for cost in forward_costs(config, 2, fused_tail).values():
         total += cost.launches_per_forward * max(cost.flops / PEAK_FP16_MFMA_FLOPS, cost.bytes / PEAK_HBM_BYTES)
     return total * microbatches
 
