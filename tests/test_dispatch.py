@@ -1,0 +1,85 @@
+"""Shape-dispatch table (CPU): routes, support limits, and agreement with the library's tables."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from tiktoktechjam2026_amd import dispatch
+from tiktoktechjam2026_amd.config import BENCHMARK_CONFIGS, TransformerConfig
+from tiktoktechjam2026_amd.mixed_precision import MixedPrecisionTransformer
+
+
+def test_benchmark_config_routes():
+    fused = {name: dispatch.plan(cfg).fuse_layer_tail for name, cfg in BENCHMARK_CONFIGS.items()}
+    assert fused == {"cfg1": True, "cfg2": True, "cfg3": True, "cfg4": False, "cfg5": False}
+    for cfg in BENCHMARK_CONFIGS.values():
+        route = dispatch.plan(cfg)
+        assert route.supported and route.fuse_attention_output_norm and route.fuse_full_ffn
+        assert route.normalized_dtype == torch.float16
+
+
+def test_enable_flags_change_the_route():
+    cfg = BENCHMARK_CONFIGS["cfg2"]
+    assert not dispatch.plan(cfg, enable_full_ffn_fusion=False).fuse_layer_tail
+    r = dispatch.plan(cfg, enable_fp16_custom_attention=False)
+    assert not r.fp16_attention and not r.fuse_layer_tail
+    r = dispatch.plan(cfg, enable_fp16_normalized_stream=False)
+    assert r.normalized_dtype == torch.float32 and not r.fuse_layer_tail
+
+
+@pytest.mark.parametrize("d,h,ok", [(128, 4, True), (96, 3, True), (128, 16, False), (24, 3, False), (40, 5, False)])
+def test_support_limits(d, h, ok):
+    route = dispatch.plan(TransformerConfig(2, 8, d, h, 64, 1, True))
+    assert route.supported == ok
+    if not ok:
+        with pytest.raises(ValueError):
+            MixedPrecisionTransformer(TransformerConfig(2, 8, d, h, 64, 1, True))
+
+
+def test_python_tables_match_library(built_library):
+    lib = built_library
+    for d in (16, 32, 64, 96, 128, 256, 512):
+        assert bool(lib.mpk_layernorm_qkv_supported(d)) == (d in dispatch.LAYERNORM_QKV_WIDTHS)
+        for f in (32, 64, 96, 128, 256, 512, 1024, 2048):
+            assert bool(lib.mpk_layer_tail_supported(d, f)) == ((d, f) in dispatch.LAYER_TAIL_SHAPES)
+
+
+def test_model_interface_mirrors_reference():
+    cfg = BENCHMARK_CONFIGS["cfg1"]
+    model = MixedPrecisionTransformer(
+        cfg, enable_case11_schedule=True, enable_attention_output_norm_fusion=True, enable_full_ffn_fusion=True,
+        enable_fp16_custom_attention=True, enable_fp16_normalized_stream=True,
+    )
+    for attr in ("use_case8_triton", "use_d128_triton", "use_d128_custom_attention", "use_fp16_custom_attention",
+                 "use_case11_schedule", "fuse_attention_output_norm", "fuse_full_ffn", "use_fp16_normalized_stream",
+                 "use_d32_triton", "assume_all_tokens_valid"):
+        assert hasattr(model, attr)
+    keys = list(model.state_dict())
+    assert keys[:6] == ["layers.0.norm1.weight", "layers.0.norm1.bias", "layers.0.attention.qkv_proj.weight",
+                        "layers.0.attention.qkv_proj.bias", "layers.0.attention.out_proj.weight",
+                        "layers.0.attention.out_proj.bias"]
+    assert model.state_dict()["layers.0.attention.qkv_proj.weight"].shape == (384, 128)
+    model.convert_projections_to_fp16()
+    sd = model.state_dict()
+    assert sd["layers.0.attention.qkv_proj.weight"].dtype == torch.float16
+    assert sd["layers.0.ffn_out.bias"].dtype == torch.float16
+    assert sd["layers.0.norm2.weight"].dtype == torch.float32
+    with pytest.raises(ValueError):
+        model(torch.zeros(1, 2, 128, dtype=torch.float16))
+
+
+def test_copy_weights_packs_qkv():
+    from oracle import strict_fp32
+    from tiktoktechjam2026_amd.mixed_precision import copy_mixed_model_weights
+
+    cfg = TransformerConfig(1, 4, 32, 2, 64, 2, True)
+    state = strict_fp32.seeded_state_dict(cfg, 9)
+    model = MixedPrecisionTransformer(cfg)
+    copy_mixed_model_weights(state, model)
+    packed = model.state_dict()["layers.1.attention.qkv_proj.weight"]
+    assert torch.equal(packed[:32], state["layers.1.attention.q_proj.weight"])
+    assert torch.equal(packed[32:64], state["layers.1.attention.k_proj.weight"])
+    assert torch.equal(packed[64:], state["layers.1.attention.v_proj.weight"])
+    assert torch.equal(model.state_dict()["layers.1.attention.qkv_proj.bias"][64:],
+                       state["layers.1.attention.v_proj.bias"])

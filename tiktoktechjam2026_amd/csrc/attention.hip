@@ -47,8 +47,10 @@ struct AttnShape {
   static constexpr int LDK = HD + 8;   // K tile row stride (halves)
   static constexpr int LDV = KT + 8;   // V^T tile row stride (halves)
   static constexpr int CPK = HD / 8;   // 8-element chunks per key row
-  static constexpr int CHUNKS = KT * CPK;
+  static constexpr int CHUNKS = KT * CPK;                           // K tile: one 16-byte chunk per item
   static constexpr int PER_THREAD = (CHUNKS + kBlock - 1) / kBlock;
+  static constexpr int VITEMS = (KT / 2) * CPK;                     // V tile: a key pair x one chunk per item
+  static constexpr int V_PER_THREAD = (VITEMS + kBlock - 1) / kBlock;
   static constexpr int DT = HD >= 32 ? HD / 32 : 1;  // output d tiles (pairs of 16, or one tile of 16)
 };
 
@@ -120,7 +122,11 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
   const int ntiles = (kv_end + KT - 1) / KT;
 
   // ---- register prefetch of one K/V tile ----
-  h8 kreg[SH::PER_THREAD], vreg[SH::PER_THREAD];
+  // K items: one 16-byte chunk of one key row, stored as-is.  V items: the same
+  // chunk of two consecutive keys, stored transposed as 8 dwords (d, key pair),
+  // so a wave's 64 lanes write 32 consecutive key pairs of two d rows per
+  // instruction - no bank conflicts, and a quarter of the 16-bit stores.
+  h8 kreg[SH::PER_THREAD], vreg[SH::V_PER_THREAD][2];
   float breg = 0.f;
   auto fetch = [&](int kb) {
 #pragma unroll
@@ -128,9 +134,16 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
       const int c = threadIdx.x + i * kBlock;
       const int key = c / SH::CPK, col = (c % SH::CPK) * 8;
       const int gk = kb + key;
-      const bool ok = c < SH::CHUNKS && gk < S;
-      kreg[i] = ok ? load8_as_half(Kp + (int64_t)gk * a.ks[2] + col) : zero_h8();
-      vreg[i] = ok ? load8_as_half(Vp + (int64_t)gk * a.vs[2] + col) : zero_h8();
+      kreg[i] = c < SH::CHUNKS && gk < S ? load8_as_half(Kp + (int64_t)gk * a.ks[2] + col) : zero_h8();
+    }
+#pragma unroll
+    for (int i = 0; i < SH::V_PER_THREAD; ++i) {
+      const int c = threadIdx.x + i * kBlock;
+      const int kp = c % (KT / 2), col = (c / (KT / 2)) * 8;
+      const int gk = kb + 2 * kp;
+      const bool ok = c < SH::VITEMS;
+      vreg[i][0] = ok && gk < S ? load8_as_half(Vp + (int64_t)gk * a.vs[2] + col) : zero_h8();
+      vreg[i][1] = ok && gk + 1 < S ? load8_as_half(Vp + (int64_t)(gk + 1) * a.vs[2] + col) : zero_h8();
     }
     if (threadIdx.x < KT) {
       const int gk = kb + threadIdx.x;
@@ -146,8 +159,21 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
       if (c < SH::CHUNKS) {
         const int key = c / SH::CPK, col = (c % SH::CPK) * 8;
         *reinterpret_cast<h8*>(&ks_lds[key * SH::LDK + col]) = kreg[i];
+      }
+    }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) vt_lds[(col + j) * SH::LDV + key] = vreg[i][j];
+    for (int i = 0; i < SH::V_PER_THREAD; ++i) {
+      const int c = threadIdx.x + i * kBlock;
+      if (c < SH::VITEMS) {
+        const int kp = c % (KT / 2), col = (c / (KT / 2)) * 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+          h2 pair;
+          pair[0] = vreg[i][0][j];
+          pair[1] = vreg[i][1][j];
+          *reinterpret_cast<h2*>(&vt_lds[(col + j) * SH::LDV + 2 * kp]) = pair;
+        }
       }
     }
     if (threadIdx.x < KT) kbias[threadIdx.x] = breg;
