@@ -20,7 +20,8 @@
 // cross-lane shuffles, and fp16(P) is already laid out as the B operand of
 // O^T = V^T P^T.  Key tiles strictly above a wave's queries are skipped; only
 // tiles that straddle the diagonal (or the sequence end, or carry a key mask)
-// pay for masking.  Workgroups are issued longest-first (last query block first).
+// pay for masking.  Query blocks are issued longest first, and each XCD owns a
+// contiguous range of (batch, head) rows so they share K/V through its L2.
 #include "mpk_common.h"
 
 namespace mpk {
@@ -67,8 +68,20 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
   const int S = a.seq;
   const int BH = a.batch * a.heads;
   const int nqb = (S + QB - 1) / QB;
-  const int qblock = nqb - 1 - (int)(blockIdx.x / BH);
-  const int bh = blockIdx.x % BH;
+  // Workgroups are dispatched round-robin over the 8 XCDs.  Each XCD gets a
+  // contiguous range of (batch, head) rows - neighbouring heads share 128-byte
+  // lines of the packed QKV rows - and walks its range longest query block
+  // first, so the blocks of one row run close together on one L2.
+  int bh, qblock;
+  if ((BH & 7) == 0) {
+    const int per_xcd = BH >> 3;
+    const int slot = blockIdx.x >> 3;
+    bh = (blockIdx.x & 7) * per_xcd + slot % per_xcd;
+    qblock = nqb - 1 - slot / per_xcd;
+  } else {
+    bh = blockIdx.x % BH;
+    qblock = nqb - 1 - (int)(blockIdx.x / BH);
+  }
   const int b = bh / a.heads, h = bh % a.heads;
   const int q0 = qblock * QB;
 

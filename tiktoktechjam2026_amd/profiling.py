@@ -196,3 +196,128 @@ def describe_rate(value: float) -> str:
     if not math.isfinite(value):
         return "n/a"
     return f"{value:,.0f}"
+
+
+# --------------------------------------------------------------------------- PMC traffic helpers
+#
+#   python -m tiktoktechjam2026_amd.profiling run --config cfg2 --iters 3
+#       runs the configured forward eagerly (no graphs) for PMC collection, after a plain
+#       device copy of 1 GiB (the calibration kernel: 1 GiB read + 1 GiB written).
+#   python -m tiktoktechjam2026_amd.profiling summarize FETCH.csv WRITE.csv --config cfg2 --out J
+#       turns two rocprofv3 --pmc counter CSVs (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch)
+#       into HBM bytes per launch per kernel, each counter scaled by copy_bytes / counter(copy).
+
+_KERNEL_KEYS = (
+    ("layer_tail_kernel<128, 32, 1, false", "layernorm_qkv"),
+    ("layer_tail_kernel", "layer_tail"),
+    ("attention_kernel", "attention"),
+    ("linear_kernel", "linear"),
+    ("ffn_ln_kernel", "ffn_ln"),
+    ("residual_layernorm_kernel", "layernorm"),
+)
+CALIBRATION_BYTES = 1 << 30
+
+
+def _kernel_key(name: str) -> str:
+    if "layer_tail_kernel" in name and ", true, true," in name:
+        return "layer_tail_last"
+    for pattern, key in _KERNEL_KEYS:
+        if pattern in name:
+            return key
+    if "copyBuffer" in name or "copy_kernel" in name or "elementwise_kernel" in name:
+        return "copy"
+    return name[:60]
+
+
+def _run(config_name: str, iters: int) -> None:
+    from .config import BENCHMARK_CONFIGS
+    from . import harness
+    from .mixed_precision import MixedPrecisionTransformer, copy_mixed_model_weights
+
+    dev = torch.device("cuda:0")
+    src = torch.empty(CALIBRATION_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)  # calibration kernel
+    torch.cuda.synchronize()
+    del src, dst
+    config = BENCHMARK_CONFIGS[config_name]
+    if config.batch_size * config.seq_len > 262144:
+        import dataclasses
+
+        config = dataclasses.replace(config, batch_size=262144 // config.seq_len)
+    model = MixedPrecisionTransformer(config)
+    copy_mixed_model_weights(harness.seeded_reference_state_dict(config, 1234), model)
+    model = model.to(dev).eval()
+    model.convert_projections_to_fp16()
+    x, _ = harness.generate_random_case(config, dev, torch.float32, 1234 + 100000, 0.0, 1.0)
+    with torch.inference_mode():
+        for _ in range(iters):
+            model(x)
+    torch.cuda.synchronize()
+
+
+def _summarize(fetch_csv: str, write_csv: str, config_name: str, out: str) -> None:
+    import csv
+    import json
+    from collections import defaultdict
+
+    def per_kernel(path: str, counter: str):
+        sums, counts, peak = defaultdict(float), defaultdict(int), defaultdict(float)
+        with open(path) as handle:
+            for row in csv.DictReader(handle):
+                if row["Counter_Name"] != counter:
+                    continue
+                key = _kernel_key(row["Kernel_Name"])
+                value = float(row["Counter_Value"])
+                sums[key] += value
+                counts[key] += 1
+                peak[key] = max(peak[key], value)
+        out = {k: sums[k] / counts[k] for k in sums}
+        if "copy" in peak:
+            out["copy"] = peak["copy"]  # the 1 GiB calibration copy is the largest copy dispatch
+        return out
+
+    fetch = per_kernel(fetch_csv, "FETCH_SIZE")
+    write = per_kernel(write_csv, "WRITE_SIZE")
+    # the calibration copy is the largest "copy" dispatch; its counters should read 1 GiB each
+    f_scale = CALIBRATION_BYTES / (fetch["copy"] * 1024.0) if fetch.get("copy") else 1.0
+    w_scale = CALIBRATION_BYTES / (write["copy"] * 1024.0) if write.get("copy") else 1.0
+    table = {"calibration": {"copy_bytes": CALIBRATION_BYTES, "fetch_scale": f_scale, "write_scale": w_scale}}
+    entry = {}
+    for key in sorted(set(fetch) | set(write)):
+        if key == "copy":
+            continue
+        fb = fetch.get(key, 0.0) * 1024.0 * f_scale
+        wb = write.get(key, 0.0) * 1024.0 * w_scale
+        entry[key] = {"fetch_bytes": fb, "write_bytes": wb, "bytes_per_launch": fb + wb}
+    table[config_name] = entry
+    try:
+        with open(out) as handle:
+            old = json.load(handle)
+    except (OSError, ValueError):
+        old = {}
+    old.update(table)
+    with open(out, "w") as handle:
+        json.dump(old, handle, indent=1, sort_keys=True)
+    print(json.dumps(table, indent=1))
+
+
+if __name__ == "__main__":
+    import argparse
+
+    parser = argparse.ArgumentParser()
+    sub = parser.add_subparsers(dest="cmd", required=True)
+    p_run = sub.add_parser("run")
+    p_run.add_argument("--config", default="cfg2")
+    p_run.add_argument("--iters", type=int, default=3)
+    p_sum = sub.add_parser("summarize")
+    p_sum.add_argument("fetch_csv")
+    p_sum.add_argument("write_csv")
+    p_sum.add_argument("--config", default="cfg2")
+    p_sum.add_argument("--out", default="profiles/hbm_traffic.json")
+    args = parser.parse_args()
+    if args.cmd == "run":
+        _run(args.config, args.iters)
+    else:
+        _summarize(args.fetch_csv, args.write_csv, args.config, args.out)
