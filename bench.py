@@ -184,11 +184,14 @@ def main(argv=None) -> int:
         "algorithmic_flops": dominant["flops"],
         "algorithmic_bytes": dominant["bytes"],
     }
-    forward_floor_ms = (
-        profiling.forward_roofline_seconds(
-            config, max(1, config.batch_size // micro) if micro else 1, model.route.fuse_layer_tail
-        ) * 1e3
-    )
+    if micro:
+        import dataclasses
+
+        per_micro = dataclasses.replace(config, batch_size=micro)
+        floor_s = profiling.forward_roofline_seconds(per_micro, config.batch_size // micro, model.route.fuse_layer_tail)
+    else:
+        floor_s = profiling.forward_roofline_seconds(config, 1, model.route.fuse_layer_tail)
+    forward_floor_ms = floor_s * 1e3
 
     # ---- CPU baseline (strict-FP32 oracle, bounded sample) + parity on the sampled rows ----
     cpu_baseline = None

@@ -5,19 +5,20 @@
 //   _causal_attention_fp16_fwd  custom_kernel/triton_attention.py:126-232  (FP16 I/O)
 //   _causal_attention_fwd       custom_kernel/triton_attention.py:16-123   (FP32 I/O)
 // Math per query row (same rounding points as the FP16 reference kernel):
-//   s_j = q . k_j  (FP16 operands, FP32 accumulate)
-//   m   = running max of s (FP32, raised lazily);  p_j = 2^(s_j*c - m*c), c = scale*log2(e)
+//   s_j*c = (q*c) . k_j  (FP16 operands: q*c split into hi + lo; FP32 accumulate)
+//   m   = running max of s*c (FP32, raised lazily);  p_j = 2^(s_j*c - m), c = scale*log2(e)
 //   l   = running sum of p_j in FP32;  acc += fp16(p_j) * v_j  (FP32 accumulate)
 //   o   = acc / l, rounded to the output type.
 // For FP32 inputs (the reference's TF32 kernel) q, k, v are rounded to FP16 on
 // load, which keeps the same 10-bit operand mantissa as TF32.
 //
-// Structure.  A workgroup (4 waves) owns QB = 64*QT queries of one (batch, head);
-// each wave owns 16*QT queries.  Key/value tiles of 64 rows are staged through
-// LDS (K row-major, V transposed) with a one-tile register prefetch.  Each wave
+// Structure.  A workgroup of NW waves owns QB = 16*QT*NW queries of one
+// (batch, head); each wave owns 16*QT queries.  Key/value tiles of KTILE rows
+// are staged through double-buffered LDS (K row-major, V transposed as key
+// pairs) with a one-tile register prefetch and ONE barrier per tile.  Each wave
 // computes S^T = K Q^T with the paired row mapping (mpk_common.h), so a lane
 // holds one query and 8 consecutive keys per 32-key pair: the row max needs two
-// cross-lane shuffles, and fp16(P) is already laid out as the B operand of
+// cross-lane swaps, and fp16(P) is already laid out as the B operand of
 // O^T = V^T P^T.  Key tiles strictly above a wave's queries are skipped; only
 // tiles that straddle the diagonal (or the sequence end, or carry a key mask)
 // pay for masking.  Query blocks are issued longest first, and each XCD owns a
@@ -26,10 +27,7 @@
 
 namespace mpk {
 
-constexpr int KT = 64;  // keys per tile
-// Initial running max: finite so that a row whose keys are all masked so far
-// still gives exp2(-inf - kNoMax*c) = 0 instead of NaN.
-constexpr float kNoMax = -1.0e30f;
+// The running max (log2 units) is raised only when a tile exceeds it by more than this.
 constexpr float kRescaleLog2 = 8.0f;
 
 struct AttnArgs {
@@ -43,27 +41,33 @@ struct AttnArgs {
   float c;  // scale * log2(e)
 };
 
-template <int HD>
+template <int HD, int KTILE, int NT>
 struct AttnShape {
-  static constexpr int LDK = HD + 8;   // K tile row stride (halves)
-  static constexpr int LDV = KT + 8;   // V^T tile row stride (halves)
-  static constexpr int CPK = HD / 8;   // 8-element chunks per key row
-  static constexpr int CHUNKS = KT * CPK;                           // K tile: one 16-byte chunk per item
-  static constexpr int PER_THREAD = (CHUNKS + kBlock - 1) / kBlock;
-  static constexpr int VITEMS = (KT / 2) * CPK;                     // V tile: a key pair x one chunk per item
-  static constexpr int V_PER_THREAD = (VITEMS + kBlock - 1) / kBlock;
+  static constexpr int LDK = HD + 8;      // K tile row stride (halves)
+  static constexpr int LDV = KTILE + 8;   // V^T tile row stride (halves)
+  static constexpr int CPK = HD / 8;      // 8-element chunks per key row
+  static constexpr int CHUNKS = KTILE * CPK;                     // K tile: one 16-byte chunk per item
+  static constexpr int PER_THREAD = (CHUNKS + NT - 1) / NT;
+  static constexpr int VITEMS = (KTILE / 2) * CPK;               // V tile: a key pair x one chunk per item
+  static constexpr int V_PER_THREAD = (VITEMS + NT - 1) / NT;
   static constexpr int DT = HD >= 32 ? HD / 32 : 1;  // output d tiles (pairs of 16, or one tile of 16)
+  static constexpr int NP = KTILE / 32;              // key pairs per tile
+  static constexpr int KBUF = KTILE * LDK;
+  static constexpr int VBUF = HD * LDV;
 };
 
-template <int HD, int QT, typename IT, typename OT, bool KEYMASK>
-__global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
-  using SH = AttnShape<HD>;
-  constexpr int QB = 64 * QT;
+template <int HD, int QT, int KTILE, int NW, typename IT, typename OT, bool KEYMASK>
+__global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
+  constexpr int NT = 64 * NW;
+  using SH = AttnShape<HD, KTILE, NT>;
+  constexpr int QB = 16 * QT * NW;
+  constexpr int NP = SH::NP;
   static_assert(HD == 16 || HD == 32 || HD == 64 || HD == 128, "head dim");
+  static_assert(KTILE % 32 == 0 && KTILE <= NT, "key tile");
 
-  __shared__ _Float16 ks_lds[KT * SH::LDK];
-  __shared__ _Float16 vt_lds[HD * SH::LDV];
-  __shared__ float kbias[KT];
+  __shared__ _Float16 ks_lds[2][SH::KBUF];
+  __shared__ _Float16 vt_lds[2][SH::VBUF];
+  __shared__ float kbias[2][KTILE];
 
   const int S = a.seq;
   const int BH = a.batch * a.heads;
@@ -97,148 +101,168 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
   const int qw_last = qw0 + 16 * QT - 1;     // last query of this wave
 
   // ---- Q fragments (B operand of S^T = K Q^T), kept in registers ----
+  // q is pre-multiplied by c = scale*log2(e) in FP32 and split into FP16 hi + lo
+  // (hi + lo = q*c to ~2^-22 relative), so two MFMAs give s*c - m directly in
+  // the FP32 accumulator (which starts at -m): no per-score scaling FMA, and the
+  // exponent argument is more accurate than rounding s*c separately.
   constexpr int QK_STEPS = HD >= 32 ? HD / 32 : 1;
-  h8 qf[QT][QK_STEPS];
-  h4 qf16[QT];
+  h8 qh[QT][QK_STEPS], ql[QT][QK_STEPS];
+  h4 qh16[QT], ql16[QT];
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     const int q = qw0 + 16 * t + r;
     if constexpr (HD == 16) {
-      h4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = (_Float16)0.f;
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
       if (q < S) {
         const IT* src = Q + (int64_t)q * a.qs[2] + 4 * g;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = (_Float16)src[j];
+        for (int j = 0; j < 4; ++j) v[j] = (float)(_Float16)src[j] * a.c;
       }
-      qf16[t] = v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        qh16[t][j] = (_Float16)v[j];
+        ql16[t][j] = (_Float16)(v[j] - (float)qh16[t][j]);
+      }
     } else {
 #pragma unroll
-      for (int kq = 0; kq < QK_STEPS; ++kq)
-        qf[t][kq] = q < S ? load8_as_half(Q + (int64_t)q * a.qs[2] + kq * 32 + 8 * g) : zero_h8();
+      for (int kq = 0; kq < QK_STEPS; ++kq) {
+        const h8 raw = q < S ? load8_as_half(Q + (int64_t)q * a.qs[2] + kq * 32 + 8 * g) : zero_h8();
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float v = (float)raw[j] * a.c;
+          qh[t][kq][j] = (_Float16)v;
+          ql[t][kq][j] = (_Float16)(v - (float)qh[t][kq][j]);
+        }
+      }
     }
   }
 
-  // ---- running statistics and output accumulators ----
-  float m_run[QT], l_run[QT];
+  // ---- running statistics (log2 units) and output accumulators ----
+  // mrow: running max of s*c for the query row; fresh: the row has not seen a
+  // visible key yet (its tiles are computed without the -mrow offset).
+  float mrow[QT], l_run[QT];
+  bool fresh[QT];
   f4 oacc[QT][SH::DT][2];
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
-    m_run[t] = kNoMax;
+    mrow[t] = 0.f;
+    fresh[t] = true;
     l_run[t] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < SH::DT; ++dt) oacc[t][dt][0] = oacc[t][dt][1] = zero4();
   }
 
   const int kv_end = a.causal ? min(q0 + QB, S) : S;  // keys [0, kv_end) can matter
-  const int ntiles = (kv_end + KT - 1) / KT;
+  const int ntiles = (kv_end + KTILE - 1) / KTILE;
 
   // ---- register prefetch of one K/V tile ----
   // K items: one 16-byte chunk of one key row, stored as-is.  V items: the same
   // chunk of two consecutive keys, stored transposed as 8 dwords (d, key pair),
-  // so a wave's 64 lanes write 32 consecutive key pairs of two d rows per
+  // so a wave's 64 lanes write consecutive key pairs of two d rows per
   // instruction - no bank conflicts, and a quarter of the 16-bit stores.
   h8 kreg[SH::PER_THREAD], vreg[SH::V_PER_THREAD][2];
   float breg = 0.f;
   auto fetch = [&](int kb) {
 #pragma unroll
     for (int i = 0; i < SH::PER_THREAD; ++i) {
-      const int c = threadIdx.x + i * kBlock;
+      const int c = threadIdx.x + i * NT;
       const int key = c / SH::CPK, col = (c % SH::CPK) * 8;
       const int gk = kb + key;
       kreg[i] = c < SH::CHUNKS && gk < S ? load8_as_half(Kp + (int64_t)gk * a.ks[2] + col) : zero_h8();
     }
 #pragma unroll
     for (int i = 0; i < SH::V_PER_THREAD; ++i) {
-      const int c = threadIdx.x + i * kBlock;
-      const int kp = c % (KT / 2), col = (c / (KT / 2)) * 8;
+      const int c = threadIdx.x + i * NT;
+      const int kp = c % (KTILE / 2), col = (c / (KTILE / 2)) * 8;
       const int gk = kb + 2 * kp;
       const bool ok = c < SH::VITEMS;
       vreg[i][0] = ok && gk < S ? load8_as_half(Vp + (int64_t)gk * a.vs[2] + col) : zero_h8();
       vreg[i][1] = ok && gk + 1 < S ? load8_as_half(Vp + (int64_t)(gk + 1) * a.vs[2] + col) : zero_h8();
     }
-    if (threadIdx.x < KT) {
+    if (threadIdx.x < KTILE) {
       const int gk = kb + threadIdx.x;
       bool valid = gk < S;
       if (KEYMASK && valid) valid = kv_valid[gk] != 0;
       breg = valid ? 0.f : -INFINITY;
     }
   };
-  auto stash = [&]() {
+  auto stash = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < SH::PER_THREAD; ++i) {
-      const int c = threadIdx.x + i * kBlock;
+      const int c = threadIdx.x + i * NT;
       if (c < SH::CHUNKS) {
         const int key = c / SH::CPK, col = (c % SH::CPK) * 8;
-        *reinterpret_cast<h8*>(&ks_lds[key * SH::LDK + col]) = kreg[i];
+        *reinterpret_cast<h8*>(&ks_lds[buf][key * SH::LDK + col]) = kreg[i];
       }
     }
 #pragma unroll
     for (int i = 0; i < SH::V_PER_THREAD; ++i) {
-      const int c = threadIdx.x + i * kBlock;
+      const int c = threadIdx.x + i * NT;
       if (c < SH::VITEMS) {
-        const int kp = c % (KT / 2), col = (c / (KT / 2)) * 8;
+        const int kp = c % (KTILE / 2), col = (c / (KTILE / 2)) * 8;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           typedef _Float16 h2 __attribute__((ext_vector_type(2)));
           h2 pair;
           pair[0] = vreg[i][0][j];
           pair[1] = vreg[i][1][j];
-          *reinterpret_cast<h2*>(&vt_lds[(col + j) * SH::LDV + 2 * kp]) = pair;
+          *reinterpret_cast<h2*>(&vt_lds[buf][(col + j) * SH::LDV + 2 * kp]) = pair;
         }
       }
     }
-    if (threadIdx.x < KT) kbias[threadIdx.x] = breg;
+    if (threadIdx.x < KTILE) kbias[buf][threadIdx.x] = breg;
   };
 
-  fetch(0);
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int kb = tile * KT;
-    __syncthreads();
-    stash();
-    __syncthreads();
-    if (tile + 1 < ntiles) fetch(kb + KT);
+  // ---- one key tile: S^T, online softmax, O^T += V^T P^T ----
+  auto process = [&](const int kb, const _Float16* ksb, const _Float16* vtb, const float* kbb) {
+    if (a.causal && kb > qw_last) return;  // whole tile is in this wave's future
+    const bool need_causal = a.causal && kb + KTILE - 1 > qw0;  // tile straddles this wave's diagonal
+    const bool need_bias = KEYMASK || kb + KTILE > S;          // padded keys or keys past the end
 
-    if (a.causal && kb > qw_last) continue;  // whole tile is in this wave's future
-    const bool need_causal = a.causal && kb + KT - 1 > qw0;  // tile straddles this wave's diagonal
-    const bool need_bias = KEYMASK || kb + KT > S;          // padded keys or keys past the end
-
-    // ---- S^T = K Q^T for 64 keys x 16*QT queries ----
-    f4 sc[2][2][QT];  // [key pair][tile in pair][q tile]
+    // S^T = K (Q*c)^T - m for KTILE keys x 16*QT queries
+    f4 sc[NP][2][QT];  // [key pair][tile in pair][q tile]
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int p = 0; p < NP; ++p)
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         const int krow = 32 * p + pair_row(r, tt);
 #pragma unroll
-        for (int t = 0; t < QT; ++t) sc[p][tt][t] = zero4();
+        for (int t = 0; t < QT; ++t) {
+          const float c0 = fresh[t] ? 0.f : -mrow[t];
+          sc[p][tt][t] = f4{c0, c0, c0, c0};
+        }
         if constexpr (HD == 16) {
-          const h4 ka = *reinterpret_cast<const h4*>(&ks_lds[krow * SH::LDK + 4 * g]);
+          const h4 ka = *reinterpret_cast<const h4*>(&ksb[krow * SH::LDK + 4 * g]);
 #pragma unroll
-          for (int t = 0; t < QT; ++t) sc[p][tt][t] = mfma16(ka, qf16[t], sc[p][tt][t]);
+          for (int t = 0; t < QT; ++t) {
+            sc[p][tt][t] = mfma16(ka, qh16[t], sc[p][tt][t]);
+            sc[p][tt][t] = mfma16(ka, ql16[t], sc[p][tt][t]);
+          }
         } else {
 #pragma unroll
           for (int kq = 0; kq < QK_STEPS; ++kq) {
-            const h8 ka = *reinterpret_cast<const h8*>(&ks_lds[krow * SH::LDK + kq * 32 + 8 * g]);
+            const h8 ka = *reinterpret_cast<const h8*>(&ksb[krow * SH::LDK + kq * 32 + 8 * g]);
 #pragma unroll
-            for (int t = 0; t < QT; ++t) sc[p][tt][t] = mfma32(ka, qf[t][kq], sc[p][tt][t]);
+            for (int t = 0; t < QT; ++t) {
+              sc[p][tt][t] = mfma32(ka, qh[t][kq], sc[p][tt][t]);
+              sc[p][tt][t] = mfma32(ka, ql[t][kq], sc[p][tt][t]);
+            }
           }
         }
       }
 
-    // ---- online softmax, per query tile ----
-    // The running max is only raised when the tile max exceeds it by more than
-    // kRescaleLog2 (log2 units); otherwise the stale max is kept and p may reach
-    // 2^kRescaleLog2.  acc and l carry the same scale, so o = acc / l is unchanged.
-    h8 pf[QT][2];  // fp16(P) as the B operand of the PV product, per key pair
+    // Online softmax.  Scores arrive as s*c - mrow.  The running max is only
+    // raised when a tile exceeds it by more than kRescaleLog2; otherwise the
+    // stale max is kept and p may reach 2^kRescaleLog2.  acc and l share the
+    // scale, so o = acc / l is unchanged.  Fresh rows adopt their first finite max.
+    h8 pf[QT][NP];  // fp16(P) as the B operand of the PV product, per key pair
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
       if (need_causal) {
         // key kb + 32p + 8g + 4tt + i is visible iff it is <= query qw0 + 16t + r
         const int lim = qw0 + 16 * t + r - kb - 8 * g;
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
+        for (int p = 0; p < NP; ++p)
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -247,51 +271,62 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
       }
       if (need_bias) {
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
+        for (int p = 0; p < NP; ++p)
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sc[p][tt][t][i] += kbias[32 * p + 8 * g + 4 * tt + i];
+            for (int i = 0; i < 4; ++i) sc[p][tt][t][i] += kbb[32 * p + 8 * g + 4 * tt + i];
       }
       float mx = sc[0][0][t][0];
 #pragma unroll
-      for (int p = 0; p < 2; ++p)
+      for (int p = 0; p < NP; ++p)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[p][tt][t][i]);
       mx = max_over_groups(mx);
-      const float m_cand = fmaxf(m_run[t], mx);
-      if ((m_cand - m_run[t]) * a.c > kRescaleLog2) {
-        const float alpha = __builtin_amdgcn_exp2f((m_run[t] - m_cand) * a.c);
-        m_run[t] = m_cand;
-        l_run[t] *= alpha;
+      const bool shift_row = fresh[t] ? (mx > -INFINITY) : (mx > kRescaleLog2);
+      if (__builtin_amdgcn_ballot_w64(shift_row)) {  // rare after the first tile
+        const float shift = shift_row ? mx : 0.f;
+        if (shift_row && !fresh[t]) {
+          const float alpha = __builtin_amdgcn_exp2f(-shift);
+          l_run[t] *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < SH::DT; ++dt) {
-          oacc[t][dt][0] *= alpha;
-          oacc[t][dt][1] *= alpha;
+          for (int dt = 0; dt < SH::DT; ++dt) {
+            oacc[t][dt][0] *= alpha;
+            oacc[t][dt][1] *= alpha;
+          }
         }
+        if (shift_row) {
+          mrow[t] = fresh[t] ? shift : mrow[t] + shift;
+          fresh[t] = false;
+        }
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[p][tt][t][i] -= shift;
       }
-      const float moff = -m_run[t] * a.c;
       float psum = 0.f;
 #pragma unroll
-      for (int p = 0; p < 2; ++p)
+      for (int p = 0; p < NP; ++p)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float pv = __builtin_amdgcn_exp2f(fmaf(sc[p][tt][t][i], a.c, moff));
+            const float pv = __builtin_amdgcn_exp2f(sc[p][tt][t][i]);
             psum += pv;
             pf[t][p][4 * tt + i] = (_Float16)pv;
           }
       l_run[t] += psum;
     }
 
-    // ---- O^T += V^T P^T ----
+    // O^T += V^T P^T
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
+    for (int p = 0; p < NP; ++p) {
       if constexpr (HD == 16) {
-        const h8 va = *reinterpret_cast<const h8*>(&vt_lds[r * SH::LDV + 32 * p + 8 * g]);
+        const h8 va = *reinterpret_cast<const h8*>(&vtb[r * SH::LDV + 32 * p + 8 * g]);
 #pragma unroll
         for (int t = 0; t < QT; ++t) oacc[t][0][0] = mfma32(va, pf[t][p], oacc[t][0][0]);
       } else {
@@ -300,12 +335,27 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt) {
             const int drow = 32 * dt + pair_row(r, tt);
-            const h8 va = *reinterpret_cast<const h8*>(&vt_lds[drow * SH::LDV + 32 * p + 8 * g]);
+            const h8 va = *reinterpret_cast<const h8*>(&vtb[drow * SH::LDV + 32 * p + 8 * g]);
 #pragma unroll
             for (int t = 0; t < QT; ++t) oacc[t][dt][tt] = mfma32(va, pf[t][p], oacc[t][dt][tt]);
           }
       }
     }
+  };
+
+  // Double-buffered pipeline, one barrier per tile: tile i+1 is fetched into
+  // registers while tile i is processed, then staged into the other buffer
+  // (last read in iteration i-1, which every wave left before the barrier).
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int tile = 0; tile < ntiles; ++tile) {
+    const int cur = tile & 1;
+    const bool more = tile + 1 < ntiles;
+    if (more) fetch((tile + 1) * KTILE);
+    process(tile * KTILE, ks_lds[cur], vt_lds[cur], kbias[cur]);
+    if (more) stash(cur ^ 1);
+    __syncthreads();
   }
 
   // ---- normalise and store ----
@@ -335,28 +385,42 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(AttnArgs a) {
   }
 }
 
-template <int HD, int QT, typename IT, typename OT>
+template <int HD, int QT, int KTILE, int NW, typename IT, typename OT>
 static hipError_t launch_attn(const AttnArgs& a, hipStream_t s) {
-  constexpr int QB = 64 * QT;
+  constexpr int QB = 16 * QT * NW;
   const int64_t nqb = (a.seq + QB - 1) / QB;
   const int64_t grid = nqb * a.batch * a.heads;
   if (grid > 0x7fffffff) return hipErrorInvalidConfiguration;
   if (a.key_valid)
-    hipLaunchKernelGGL((attention_kernel<HD, QT, IT, OT, true>), dim3((unsigned)grid), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((attention_kernel<HD, QT, KTILE, NW, IT, OT, true>), dim3((unsigned)grid), dim3(64 * NW), 0,
+                       s, a);
   else
-    hipLaunchKernelGGL((attention_kernel<HD, QT, IT, OT, false>), dim3((unsigned)grid), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((attention_kernel<HD, QT, KTILE, NW, IT, OT, false>), dim3((unsigned)grid), dim3(64 * NW), 0,
+                       s, a);
   return hipGetLastError();
+}
+
+// Tile variants (queries per wave x keys per tile x waves per workgroup):
+//   1: 16 x 64 x 4     2: 32 x 64 x 4     3: 32 x 128 x 4     4: 32 x 64 x 8     5: 16 x 128 x 4
+template <int HD, typename IT, typename OT>
+static hipError_t attn_variant(int variant, const AttnArgs& a, hipStream_t s) {
+  switch (variant) {
+    case 1: return launch_attn<HD, 1, 64, 4, IT, OT>(a, s);
+    case 2: return launch_attn<HD, 2, 64, 4, IT, OT>(a, s);
+    case 3: return launch_attn<HD, 2, 128, 4, IT, OT>(a, s);
+    case 4: return launch_attn<HD, 2, 64, 8, IT, OT>(a, s);
+    case 5: return launch_attn<HD, 1, 128, 4, IT, OT>(a, s);
+    default: return (hipError_t)MPK_EUNSUPPORTED;
+  }
 }
 
 template <typename IT, typename OT>
 static hipError_t attn_dispatch(int variant, const AttnArgs& a, int hd, hipStream_t s) {
-  // variant 1: 16 queries per wave; variant 2: 32 queries per wave
-  const bool two = variant == 2;
   switch (hd) {
-    case 16: return two ? launch_attn<16, 2, IT, OT>(a, s) : launch_attn<16, 1, IT, OT>(a, s);
-    case 32: return two ? launch_attn<32, 2, IT, OT>(a, s) : launch_attn<32, 1, IT, OT>(a, s);
-    case 64: return two ? launch_attn<64, 2, IT, OT>(a, s) : launch_attn<64, 1, IT, OT>(a, s);
-    case 128: return launch_attn<128, 1, IT, OT>(a, s);
+    case 16: return attn_variant<16, IT, OT>(variant, a, s);
+    case 32: return attn_variant<32, IT, OT>(variant, a, s);
+    case 64: return attn_variant<64, IT, OT>(variant, a, s);
+    case 128: return attn_variant<128, IT, OT>(variant, a, s);
     default: return (hipError_t)MPK_EUNSUPPORTED;
   }
 }
@@ -365,9 +429,12 @@ static hipError_t attn_dispatch(int variant, const AttnArgs& a, int hd, hipStrea
 
 using namespace mpk;
 
+// Built-in choice, from MI355X sweeps: short sequences favour 16 queries per wave
+// (more workgroups); long ones 32 queries per wave, and 8-wave workgroups at S >= 4096.
 extern "C" int mpk_attention_auto_variant(int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim) {
-  (void)batch; (void)heads; (void)head_dim;
-  return seq_len >= 512 && head_dim <= 64 ? 2 : 1;
+  (void)batch; (void)heads;
+  if (head_dim >= 128 || seq_len < 512) return 1;
+  return seq_len >= 4096 ? 4 : 2;
 }
 
 extern "C" int mpk_causal_attention(const void* q, const void* k, const void* v, void* o, int io_dtype,
@@ -390,7 +457,7 @@ extern "C" int mpk_causal_attention(const void* q, const void* k, const void* v,
   }
   if (batch == 0 || seq_len == 0) return MPK_OK;
   if (variant == 0) variant = mpk_attention_auto_variant(batch, heads, seq_len, head_dim);
-  if (variant != 1 && variant != 2) return MPK_EUNSUPPORTED;
+  if (variant < 1 || variant > 5) return MPK_EUNSUPPORTED;
   AttnArgs a{};
   a.q = q; a.k = k; a.v = v; a.o = o;
   for (int j = 0; j < 4; ++j) {

@@ -137,11 +137,14 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
     from .mixed_precision.hip_fused import fused_layer_tail, layer_norm_qkv
     from .mixed_precision.hip_linear import layer_norm, mixed_ffn_add_layer_norm, mixed_linear, mixed_linear_add_layer_norm
 
-    config = model.config
+    import dataclasses
+
     route = model.route
     layer = model.layers[0]
     att = layer.attention
     B, S, D = x.shape
+    # price the launches actually timed: one microbatch of B sequences
+    config = dataclasses.replace(model.config, batch_size=B) if dataclasses.is_dataclass(model.config) else model.config
     sdt = route.normalized_dtype
     causal = bool(config.causal)
     costs = forward_costs(config, 2 if sdt == torch.float16 else 4, route.fuse_layer_tail)
