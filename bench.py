@@ -188,9 +188,9 @@ def main(argv=None) -> int:
         import dataclasses
 
         per_micro = dataclasses.replace(config, batch_size=micro)
-        floor_s = profiling.forward_roofline_seconds(per_micro, config.batch_size // micro, model.route.fuse_layer_tail)
+        floor_s = profiling.forward_roofline_seconds(per_micro, config.batch_size // micro, model.route)
     else:
-        floor_s = profiling.forward_roofline_seconds(config, 1, model.route.fuse_layer_tail)
+        floor_s = profiling.forward_roofline_seconds(config, 1, model.route)
     forward_floor_ms = floor_s * 1e3
 
     # ---- CPU baseline (strict-FP32 oracle, bounded sample) + parity on the sampled rows ----

@@ -62,6 +62,16 @@ int mpk_linear(const void* x, int x_dtype, const void* w, const void* b, void* y
 int mpk_linear_auto_variant(int64_t m, int32_t n, int32_t k);
 
 /*
+ * Projection with a residual add: y = fp16(x) * w^T + b + residual  (FP32 [m, n]).
+ * residual and y are FP32 [m, n]; y may be residual itself (in-place add).  n % 8 == 0, k % 8 == 0.
+ * Replaces, fused: the unfused route's projection + residual add
+ * (mixed_precision/transformer.py:273 out_proj, whose output is added at :501-506; :669-671 ffn_out,
+ * added at :682-687); the LayerNorm of those calls follows as mpk_layernorm.
+ */
+int mpk_linear_residual(const void* x, int x_dtype, const void* w, const void* b, const float* residual, float* y,
+                        int64_t m, int32_t n, int32_t k, int variant, void* stream);
+
+/*
  * Projection + residual + LayerNorm:
  *   residual_out = fp16(x) * w^T + b + residual          (FP32)
  *   normalized_out = LayerNorm(residual_out) * gamma + beta

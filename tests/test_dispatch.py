@@ -15,7 +15,8 @@ def test_benchmark_config_routes():
     assert fused == {"cfg1": True, "cfg2": True, "cfg3": True, "cfg4": False, "cfg5": False}
     for cfg in BENCHMARK_CONFIGS.values():
         route = dispatch.plan(cfg)
-        assert route.supported and route.fuse_attention_output_norm and route.fuse_full_ffn
+        narrow = cfg.d_model < dispatch.WIDE_GEMM_FROM
+        assert route.supported and route.fuse_attention_output_norm == narrow and route.fuse_full_ffn == narrow
         assert route.normalized_dtype == torch.float16
 
 

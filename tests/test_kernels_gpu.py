@@ -111,7 +111,7 @@ def _ref_linear(x, lin, gelu):
     [(8192, 384, 128), (1000, 96, 32), (333, 2048, 512), (5, 64, 64), (4096, 128, 128), (130, 768, 256),
      (257, 40, 24)],
 )
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6, 7])
 def test_mixed_linear(hip_device, m, n, k, variant):
     from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear
 
@@ -126,6 +126,45 @@ def test_mixed_linear(hip_device, m, n, k, variant):
                 ref = _ref_linear(x32, lin, gelu)
                 tol = 1e-5 * math.sqrt(k) if out_dtype == torch.float32 else 2 ** -10
                 _close(y, ref, tol, tol, f"linear in={in_dtype} out={out_dtype} gelu={gelu}")
+
+
+@pytest.mark.parametrize(
+    "m,n,k", [(8192, 512, 2048), (777, 256, 256), (3, 136, 40), (70000, 128, 512), (4100, 1024, 264)]
+)
+@pytest.mark.parametrize("variant", [0, 1, 5, 6, 7])
+def test_mixed_linear_residual(hip_device, m, n, k, variant):
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear_residual
+
+    lin = _linear(k, n, hip_device, 17)
+    x32 = _randn((m, k), 19)
+    r32 = _randn((m, n), 23, 2.0)
+    ref = _ref_linear(x32, lin, False) + r32.double()
+    tol = 1e-5 * math.sqrt(k)
+    for in_dtype in (torch.float32, torch.float16):
+        x = x32.to(hip_device, in_dtype)
+        r = r32.to(hip_device)
+        y = mixed_linear_residual(x, lin, r, variant=variant)
+        assert y.dtype == torch.float32 and y.shape == (m, n)
+        _close(y, ref, tol, tol, f"linear+residual in={in_dtype}")
+        assert torch.equal(r.cpu(), r32), "residual input modified"
+        inplace = mixed_linear_residual(x, lin, r, out=r, variant=variant)
+        assert inplace.data_ptr() == r.data_ptr()
+        assert torch.equal(inplace.cpu(), y.cpu()), "in-place result differs"
+
+
+def test_mixed_linear_residual_rejects_bad_inputs(hip_device):
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear_residual
+
+    lin = _linear(64, 64, hip_device, 1)
+    x = torch.zeros(10, 64, device=hip_device)
+    with pytest.raises(ValueError):
+        mixed_linear_residual(x, lin, x.half())
+    with pytest.raises(ValueError):
+        mixed_linear_residual(x, lin, torch.zeros(10, 32, device=hip_device))
+    with pytest.raises(ValueError):
+        mixed_linear_residual(x, lin, x, out=torch.zeros(10, 64, device=hip_device, dtype=torch.float16))
+    with pytest.raises(RuntimeError):
+        mixed_linear_residual(x, lin, x, variant=9)
 
 
 def test_mixed_linear_3d_input(hip_device):

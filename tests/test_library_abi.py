@@ -53,6 +53,10 @@ def test_host_side_argument_rejection(built_library):
     assert lib.mpk_linear(fake, 7, fake, fake, fake, 1, 0, 10, 16, 16, 0, null) == _lib.MPK_EINVAL
     assert lib.mpk_linear(fake, 1, fake, fake, fake, 1, 0, 10, 12, 16, 0, null) == _lib.MPK_EUNSUPPORTED
     assert lib.mpk_linear(ctypes.c_void_p(72), 1, fake, fake, fake, 1, 0, 10, 16, 16, 0, null) == _lib.MPK_EALIGN
+    assert lib.mpk_linear(fake, 1, fake, fake, fake, 1, 0, 10, 16, 16, 9, null) == _lib.MPK_EUNSUPPORTED
+    assert lib.mpk_linear_residual(fake, 1, fake, fake, null, fake, 10, 16, 16, 0, null) == _lib.MPK_EINVAL
+    assert lib.mpk_linear_residual(fake, 1, fake, fake, fake, fake, 10, 20, 16, 0, null) == _lib.MPK_EUNSUPPORTED
+    assert lib.mpk_linear_residual(fake, 1, fake, fake, ctypes.c_void_p(72), fake, 10, 16, 16, 0, null) == _lib.MPK_EALIGN
     assert (
         lib.mpk_linear_residual_layernorm(fake, 1, fake, fake, fake, fake, fake, fake, fake, 1, 10, 96, 1e-5, 0, null)
         == _lib.MPK_EUNSUPPORTED

@@ -45,6 +45,10 @@ SIGNATURES = {
         [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_i64, _c_i32, _c_i32, _c_int, _c_void_p],
     ),
     "mpk_linear_auto_variant": (_c_int, [_c_i64, _c_i32, _c_i32]),
+    "mpk_linear_residual": (
+        _c_int,
+        [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i32, _c_i32, _c_int, _c_void_p],
+    ),
     "mpk_linear_residual_layernorm": (
         _c_int,
         [

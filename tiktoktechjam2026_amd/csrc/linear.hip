@@ -18,11 +18,13 @@
 // lane-local and every store is 16 (FP16) or 32 (FP32) contiguous bytes.  For
 // the LayerNorm epilogue a wave owns whole rows (BN == N), so the row
 // statistics need only two cross-lane shuffles.
+#include <algorithm>
+
 #include "mpk_common.h"
 
 namespace mpk {
 
-enum Epilogue : int { kEpiBias = 0, kEpiBiasGelu = 1, kEpiResidualLN = 2 };
+enum Epilogue : int { kEpiBias = 0, kEpiBiasGelu = 1, kEpiResidualLN = 2, kEpiBiasResidual = 3 };
 
 struct LinearArgs {
   const void* x;
@@ -113,8 +115,8 @@ __global__ __launch_bounds__(kBlock) void linear_kernel(LinearArgs a) {
     }
   }
 
-  OT* __restrict__ Y = static_cast<OT*>(a.y);
-  if constexpr (EPI == kEpiBias || EPI == kEpiBiasGelu) {
+  OT* Y = static_cast<OT*>(a.y);  // may alias a.residual (in-place residual add)
+  if constexpr (EPI == kEpiBias || EPI == kEpiBiasGelu || EPI == kEpiBiasResidual) {
 #pragma unroll
     for (int p = 0; p < PN; ++p) {
       const int n = n0 + wn * WN + 32 * p + 8 * g;
@@ -134,6 +136,12 @@ __global__ __launch_bounds__(kBlock) void linear_kernel(LinearArgs a) {
         if constexpr (EPI == kEpiBiasGelu) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) v[j] = gelu_erf(v[j]);
+        }
+        if constexpr (EPI == kEpiBiasResidual) {
+          float rv[8];
+          load8_f32(a.residual + m * N + n, rv);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] += rv[j];
         }
         store8(Y + m * N + n, v);
       }
@@ -193,6 +201,238 @@ __global__ __launch_bounds__(kBlock) void linear_kernel(LinearArgs a) {
   }
 }
 
+
+// LDS slot of weight row j: within each 32-row group, row pair_row(r, tt) goes
+// to slot 16 tt + r, so the 16 lanes of one fragment read consecutive padded
+// rows (no bank conflicts) instead of pair_row's strided set.
+__device__ __forceinline__ int w_slot(int j) {
+  return (j & ~31) | (((j >> 2) & 1) << 4) | ((j >> 3) & 3) << 2 | (j & 3);
+}
+
+// Large-tile projection for wide models: a 256 (tokens) x BN (features) output
+// tile per workgroup of 2 x BN/64 waves, each wave 128 x 64 (8 token tiles x 2
+// feature pairs).  K is staged in 64-wide chunks through LDS with a one-chunk
+// register prefetch: double-buffered with one barrier per chunk (STAGES == 2),
+// or single-buffered with two (STAGES == 1, half the LDS).  Each W fragment
+// read from LDS feeds 8 MFMAs and each X fragment 4; a 256 x 256 tile reads
+// 128 FLOPs' worth of operands per byte from L2, a 256 x 128 tile 85.
+//
+// The kernel is persistent: the grid fills the device once and each workgroup
+// walks a strided list of tiles inside its XCD's contiguous share of the tile
+// range (workgroups are dispatched to the 8 XCDs round-robin), so the tiles an
+// XCD runs at one time share token rows of X in that XCD's L2.  The chunk
+// pipeline runs across tile boundaries: the next tile's first chunk is in
+// flight while the current tile's last chunk and epilogue execute, which hides
+// the load latency that short-K projections (K = 256..512) would otherwise
+// expose once per tile.
+template <int BN, int STAGES, typename XT, int EPI, typename OT>
+__global__ __launch_bounds__(2 * BN) void linear_big_kernel(LinearArgs a) {
+  constexpr int NT = 2 * BN;                    // threads: 2 x BN/64 waves
+  constexpr int BM = 256, BK = 64, LD = BK + 16;  // 160-byte rows: conflict-free b128 LDS access
+  constexpr int WM = 128, WN = 64, TM = WM / 16, PN = WN / 32;
+  constexpr int CPR = BK / 8;                   // 8-element chunks per staged row
+  constexpr int XCH = BM * CPR / NT;            // X chunks per thread
+  constexpr int WCH = BN * CPR / NT;            // W chunks per thread
+  static_assert(XCH * NT == BM * CPR && WCH * NT == BN * CPR, "staging split");
+  static_assert(EPI != kEpiResidualLN, "row LayerNorm needs whole rows per wave");
+  static_assert(STAGES == 1 || STAGES == 2, "one or two LDS stages");
+
+  __shared__ _Float16 xs[STAGES][BM * LD];
+  __shared__ _Float16 ws[STAGES][BN * LD];
+
+  const XT* __restrict__ X = static_cast<const XT*>(a.x);
+  const _Float16* __restrict__ W = a.w;
+  const int64_t M = a.m;
+  const int N = a.n, K = a.k;
+  const int nbn = (N + BN - 1) / BN;
+  const int tiles = (int)((M + BM - 1) / BM) * nbn;
+  const int nchunks = (K + BK - 1) / BK;
+
+  // This workgroup's tiles: tile, tile + stride, ... < last.  With a grid that
+  // is a multiple of 8, XCD x (workgroups b with b % 8 == x) owns tiles
+  // [tiles x / 8, tiles (x + 1) / 8); otherwise a plain grid stride.
+  const int G = gridDim.x;
+  int tile, stride, last;
+  if ((G & 7) == 0) {
+    const int xcd = blockIdx.x & 7;
+    stride = G >> 3;
+    last = (int)((int64_t)tiles * (xcd + 1) / 8);
+    tile = (int)((int64_t)tiles * xcd / 8) + (blockIdx.x >> 3);
+  } else {
+    stride = G;
+    last = tiles;
+    tile = blockIdx.x;
+  }
+  if (tile >= last) return;                     // uniform per workgroup, before any barrier
+
+  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = l & 15, g = l >> 4;
+  const int wm = wave & 1, wn = wave >> 1;
+
+  f4 acc[PN][2][TM];
+#pragma unroll
+  for (int p = 0; p < PN; ++p)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int t = 0; t < TM; ++t) acc[p][tt][t] = zero4();
+
+  h8 xr[XCH], wr[WCH];
+  auto fetch = [&](int ftile, int k0) {
+    const int64_t fm0 = (int64_t)(ftile / nbn) * BM;
+    const int fn0 = (ftile % nbn) * BN;
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int c = threadIdx.x + i * NT;
+      const int row = c / CPR, col = (c % CPR) * 8;
+      const int64_t gm = fm0 + row;
+      const int gk = k0 + col;
+      xr[i] = gm < M && gk < K ? load8_as_half(X + gm * K + gk) : zero_h8();
+    }
+#pragma unroll
+    for (int i = 0; i < WCH; ++i) {
+      const int c = threadIdx.x + i * NT;
+      const int row = c / CPR, col = (c % CPR) * 8;
+      const int gn = fn0 + row;
+      const int gk = k0 + col;
+      wr[i] = gn < N && gk < K ? load8_as_half(W + (int64_t)gn * K + gk) : zero_h8();
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int c = threadIdx.x + i * NT;
+      *reinterpret_cast<h8*>(&xs[buf][(c / CPR) * LD + (c % CPR) * 8]) = xr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < WCH; ++i) {
+      const int c = threadIdx.x + i * NT;
+      *reinterpret_cast<h8*>(&ws[buf][w_slot(c / CPR) * LD + (c % CPR) * 8]) = wr[i];
+    }
+  };
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      // Issue every fragment read of this k-step before the first MFMA, so the
+      // LDS latency overlaps the reads still in flight instead of stalling
+      // each group of four MFMAs.
+      h8 wa[PN][2], xb[TM];
+#pragma unroll
+      for (int p = 0; p < PN; ++p)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+          wa[p][tt] = *reinterpret_cast<const h8*>(&ws[buf][(wn * WN + 32 * p + 16 * tt + r) * LD + ks * 32 + 8 * g]);
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+        xb[t] = *reinterpret_cast<const h8*>(&xs[buf][(wm * WM + 16 * t + r) * LD + ks * 32 + 8 * g]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int p = 0; p < PN; ++p)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) acc[p][tt][t] = mfma32(wa[p][tt], xb[t], acc[p][tt][t]);
+    }
+  };
+  OT* Y = static_cast<OT*>(a.y);  // may alias a.residual (in-place residual add)
+  auto epilogue = [&](int etile) {
+    const int64_t m0 = (int64_t)(etile / nbn) * BM;
+    const int n0 = (etile % nbn) * BN;
+#pragma unroll
+    for (int p = 0; p < PN; ++p) {
+      const int n = n0 + wn * WN + 32 * p + 8 * g;
+      if (n >= N) continue;
+      float bv[8];
+      load8_f16_to_f32(a.bias + n, bv);
+#pragma unroll
+      for (int t = 0; t < TM; ++t) {
+        const int64_t m = m0 + wm * WM + 16 * t + r;
+        if (m >= M) continue;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = acc[p][0][t][i] + bv[i];
+          v[4 + i] = acc[p][1][t][i] + bv[4 + i];
+        }
+        if constexpr (EPI == kEpiBiasGelu) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = gelu_erf(v[j]);
+        }
+        if constexpr (EPI == kEpiBiasResidual) {
+          float rv[8];
+          load8_f32(a.residual + m * N + n, rv);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] += rv[j];
+        }
+        store8(Y + m * N + n, v);
+      }
+    }
+  };
+
+  fetch(tile, 0);
+  stash(0);
+  __syncthreads();
+  int c = 0, buf = 0;
+  for (;;) {
+    int ntile = tile, nc = c + 1;
+    if (nc == nchunks) {
+      nc = 0;
+      ntile = tile + stride;
+    }
+    const bool more = ntile < last;
+    if (more) fetch(ntile, nc * BK);
+    compute(buf);
+    if (c == nchunks - 1) {
+      epilogue(tile);
+#pragma unroll
+      for (int p = 0; p < PN; ++p)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int t = 0; t < TM; ++t) acc[p][tt][t] = zero4();
+    }
+    if (!more) break;
+    if constexpr (STAGES == 2) {
+      buf ^= 1;
+      stash(buf);
+      __syncthreads();
+    } else {
+      __syncthreads();
+      stash(0);
+      __syncthreads();
+    }
+    tile = ntile;
+    c = nc;
+  }
+}
+
+// Workgroups that fill the device once for a persistent kernel (cached per device).
+template <typename Kernel>
+static int resident_grid(Kernel kernel, int threads, size_t lds) {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) != hipSuccess || per_cu <= 0)
+      per_cu = 1;
+    cached[dev] = cus * per_cu;
+  }
+  return cached[dev];
+}
+
+template <int BN, int STAGES, typename XT, int EPI, typename OT>
+static hipError_t launch_linear_big(const LinearArgs& a, hipStream_t s) {
+  const int64_t tiles = ((a.m + 255) / 256) * ((a.n + BN - 1) / BN);
+  if (tiles > 0x7fffffff) return hipErrorInvalidConfiguration;
+  auto kernel = linear_big_kernel<BN, STAGES, XT, EPI, OT>;
+  int64_t grid = std::min<int64_t>(tiles, resident_grid(kernel, 2 * BN, 0));
+  if (grid >= 8) grid &= ~int64_t{7};
+  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(2 * BN), 0, s, a);
+  return hipGetLastError();
+}
+
 template <int BM, int BN, int KC, int WAVES_M, typename XT, int EPI, typename OT>
 static hipError_t launch_linear(const LinearArgs& a, hipStream_t s) {
   const int64_t mb = (a.m + BM - 1) / BM;
@@ -208,6 +448,9 @@ static hipError_t launch_linear(const LinearArgs& a, hipStream_t s) {
 //   2: BM128 BN64  (4x1 waves, 32x64 per wave)   N multiple of 64
 //   3: BM128 BN32  (4x1 waves, 32x32 per wave)   narrow / ragged N
 //   4: BM64  BN128 (1x4 waves, 64x32 per wave)   short M, wide N
+//   5: BM256 BN128 (2x2 waves, 128x64 per wave, double-buffered LDS)   large M and N
+//   6: as 5 with single-buffered LDS (two workgroups per CU)
+//   7: BM256 BN256 (2x4 waves, 128x64 per wave, double-buffered LDS)
 template <typename XT, int EPI, typename OT>
 static hipError_t linear_variant(int variant, const LinearArgs& a, hipStream_t s) {
   switch (variant) {
@@ -215,6 +458,9 @@ static hipError_t linear_variant(int variant, const LinearArgs& a, hipStream_t s
     case 2: return launch_linear<128, 64, 64, 4, XT, EPI, OT>(a, s);
     case 3: return launch_linear<128, 32, 64, 4, XT, EPI, OT>(a, s);
     case 4: return launch_linear<64, 128, 64, 1, XT, EPI, OT>(a, s);
+    case 5: return launch_linear_big<128, 2, XT, EPI, OT>(a, s);
+    case 6: return launch_linear_big<128, 1, XT, EPI, OT>(a, s);
+    case 7: return launch_linear_big<256, 2, XT, EPI, OT>(a, s);
     default: return (hipError_t)MPK_EUNSUPPORTED;
   }
 }
@@ -247,7 +493,7 @@ using namespace mpk;
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 extern "C" int mpk_linear_auto_variant(int64_t m, int32_t n, int32_t k) {
-  (void)k;
+  if (n % 256 == 0 && k >= 256 && ((m + 255) / 256) * (n / 256) >= 256) return 7;
   if (n % 128 == 0 && m >= 128 * 256) return 1;
   if (n % 128 == 0) return 4;
   if (n % 64 == 0) return 2;
@@ -310,5 +556,22 @@ extern "C" int mpk_linear_residual_layernorm(const void* x, int x_dtype, const v
   const bool xf = x_dtype == kF32, of = normalized_dtype == kF32;
   if (xf) e = of ? linear_ln<float, float>(variant, a, s) : linear_ln<float, _Float16>(variant, a, s);
   else e = of ? linear_ln<_Float16, float>(variant, a, s) : linear_ln<_Float16, _Float16>(variant, a, s);
+  return (int)e;
+}
+
+extern "C" int mpk_linear_residual(const void* x, int x_dtype, const void* w, const void* b, const float* residual,
+                                   float* y, int64_t m, int32_t n, int32_t k, int variant, void* stream) {
+  if (!x || !w || !b || !residual || !y || m < 0 || n <= 0 || k <= 0) return MPK_EINVAL;
+  if (x_dtype != kF32 && x_dtype != kF16) return MPK_EINVAL;
+  if (n % 8 != 0 || k % 8 != 0) return MPK_EUNSUPPORTED;
+  if (!aligned16(x) || !aligned16(w) || !aligned16(b) || !aligned16(residual) || !aligned16(y)) return MPK_EALIGN;
+  if (m == 0) return MPK_OK;
+  if (variant == 0) variant = mpk_linear_auto_variant(m, n, k);
+  LinearArgs a{};
+  a.x = x; a.w = static_cast<const _Float16*>(w); a.bias = static_cast<const _Float16*>(b); a.y = y;
+  a.residual = residual; a.m = m; a.n = n; a.k = k;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const hipError_t e = x_dtype == kF32 ? linear_variant<float, kEpiBiasResidual, float>(variant, a, s)
+                                       : linear_variant<_Float16, kEpiBiasResidual, float>(variant, a, s);
   return (int)e;
 }

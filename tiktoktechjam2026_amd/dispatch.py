@@ -6,9 +6,14 @@ The reference selects Triton routes with hard-coded exact-shape booleans
 ops.  Here every supported shape takes the same HIP route; what varies with
 the shape is only
 
-* which fusions apply (the fused out-projection/FFN kernels cover
-  d_model in {32, 64, 128, 256, 512}; other widths use the unfused HIP
-  projection + residual-LayerNorm kernels), and
+* which fusions apply.  Up to d_model 128 the out-projection and the FFN
+  run as row-owning kernels with the residual add and LayerNorm in the
+  epilogue (``LN_FUSED_WIDTHS`` bounds what those kernels accept).  Wider
+  models (``WIDE_GEMM_FROM``) and disabled fusions run the projections as
+  large-tile GEMMs with the bias/GELU/residual add in the epilogue and a
+  separate LayerNorm: a row-owning kernel would re-read a D x D (or D x F)
+  weight for every 64-128 rows, while the GEMM tiles read it once per 256
+  rows and keep the matrix cores busy, and
 * the kernel tile variant of each launch.  Variant 0 defers to the
   library's built-in table (``mpk_*_auto_variant``); entries in ``TUNED``
   override it for shapes measured on MI355X (256 CUs, 64-lane waves).
@@ -18,7 +23,8 @@ runs 1 + 2L launches: LayerNorm+QKV, then per layer attention and the fused
 tail (out-proj+LN2+FFN+LN1'+QKV', or the final LayerNorm on the last layer).
 
 Tile variants (see the kernel sources for the exact tiles):
-  qkv / ffn-in projection  1: 128x128 (2x2 waves)  2: 128x64  3: 128x32  4: 64x128
+  projections              1: 128x128 (2x2 waves)  2: 128x64  3: 128x32  4: 64x128
+                           5: 256x128 double-buffered  6: 256x128 single-buffered
   out-proj + LN            1: 64 rows/WG           2: 128 rows/WG (d <= 128)
   fused FFN + LN           1: 16 rows/wave         2: 32 rows/wave (d <= 256)
   attention                1: 16 queries/wave      2: 32 queries/wave (hd <= 64)
@@ -38,6 +44,8 @@ ATTENTION_HEAD_DIMS = (16, 32, 64, 128)
 # must equal mpk_layer_tail_supported / mpk_layernorm_qkv_supported in the library.
 LAYER_TAIL_SHAPES = frozenset({(32, 32), (32, 64), (32, 128), (64, 64), (64, 128), (64, 256), (128, 128)})
 LAYERNORM_QKV_WIDTHS = frozenset({32, 64, 128})
+# From this width up the out-projection and FFN run as GEMMs + a separate LayerNorm.
+WIDE_GEMM_FROM = 256
 
 
 @dataclass(frozen=True)
@@ -57,6 +65,7 @@ class Route:
     ffn_variant: int = 0
     ffn_in_variant: int = 0
     ffn_out_variant: int = 0
+    out_proj_variant: int = 0
     tail_variant: int = 0
     head_variant: int = 0
     notes: Tuple[str, ...] = field(default_factory=tuple)
@@ -77,6 +86,7 @@ class Route:
                 "ffn": self.ffn_variant,
                 "ffn_in": self.ffn_in_variant,
                 "ffn_out": self.ffn_out_variant,
+                "out_proj": self.out_proj_variant,
                 "layer_tail": self.tail_variant,
                 "layernorm_qkv": self.head_variant,
             },
@@ -116,8 +126,9 @@ def plan(
         return Route(False, "d_model and ffn_dim must be multiples of 8")
     if d > 2048:
         return Route(False, "d_model above 2048")
-    fuse_out = enable_attention_output_norm_fusion and d in LN_FUSED_WIDTHS
-    fuse_ffn = enable_full_ffn_fusion and d in LN_FUSED_WIDTHS and f % 32 == 0
+    narrow = d in LN_FUSED_WIDTHS and d < WIDE_GEMM_FROM
+    fuse_out = enable_attention_output_norm_fusion and narrow
+    fuse_ffn = enable_full_ffn_fusion and narrow and f % 32 == 0
     # The layer-tail kernel chains out-proj+LN2 -> FFN+LN -> next QKV; it needs both
     # fusions, the FP16 normalized stream and FP16 attention I/O.
     fuse_tail = (

@@ -100,6 +100,49 @@ def mixed_linear(
     return output
 
 
+def mixed_linear_residual(
+    x: torch.Tensor,
+    linear: nn.Linear,
+    residual: torch.Tensor,
+    *,
+    out: Optional[torch.Tensor] = None,
+    variant: int = 0,
+) -> torch.Tensor:
+    """``fp16(x) @ W^T + b + residual`` in FP32 (the projection and residual add of the unfused route).
+
+    ``out`` may be ``residual`` itself for an in-place add.
+    """
+    if not (
+        _gpu(x)
+        and x.dtype in (torch.float16, torch.float32)
+        and _fp16_linear_ok(linear)
+        and x.shape[-1] == linear.in_features
+        and linear.in_features % 8 == 0
+        and linear.out_features % 8 == 0
+        and _gpu(residual)
+        and residual.dtype == torch.float32
+        and residual.is_contiguous()
+        and residual.shape == (*x.shape[:-1], linear.out_features)
+        and (out is None or (_gpu(out) and out.dtype == torch.float32 and out.is_contiguous()
+                             and out.shape == residual.shape))
+    ):
+        raise ValueError("unsupported mixed projection/residual inputs")
+    n_rows = x.numel() // linear.in_features
+    output = torch.empty_like(residual) if out is None else out
+    if not _aligned(x, linear.weight, linear.bias, residual, output):
+        raise ValueError("unsupported mixed projection/residual inputs (16-byte alignment)")
+    lib = _lib.load()
+    _lib.check(
+        lib.mpk_linear_residual(
+            x.data_ptr(), _lib.dtype_code(x.dtype), linear.weight.data_ptr(), linear.bias.data_ptr(),
+            residual.data_ptr(), output.data_ptr(), n_rows, linear.out_features, linear.in_features, int(variant),
+            _lib.stream_handle(x.device),
+        ),
+        "mpk_linear_residual",
+    )
+    return output
+
+
 LN_FUSED_WIDTHS = (32, 64, 128, 256, 512)
 
 

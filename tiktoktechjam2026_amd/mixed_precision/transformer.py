@@ -10,15 +10,21 @@ attributes the benchmark CLI reads, the state-dict keys and dtypes
 ``forward(x fp32 [B,S,D], valid_token_mask=None) -> fp32 [B,S,D]`` contract
 (``ValueError`` for non-FP32 input).
 
-Per layer the forward issues four HIP launches (the reference issues four
-Triton launches on its D128 routes and vendor ops elsewhere):
+Routes (chosen by ``dispatch.plan`` from the shape):
 
-  1. packed QKV projection          fp16 stream -> fp16 [T, 3D]        (mpk_linear)
-  2. causal flash attention         strided q/k/v -> fp16 [T, D]       (mpk_causal_attention)
-  3. out-projection + residual + LN -> fp32 residual, fp16 normalized (mpk_linear_residual_layernorm)
-  4. FFN + residual + next LN       -> fp32 residual, fp16 normalized (mpk_ffn_residual_layernorm)
+* layer-tail route (d_model <= 128 with the tail's weights in LDS): one
+  LayerNorm+QKV launch, then per layer the flash attention and one fused
+  out-proj + LN2 + FFN + LN1' + next-QKV kernel (mpk_layer_tail);
+* row-fused route (other d_model <= 128): per layer the QKV projection
+  (mpk_linear), attention (mpk_causal_attention), out-projection + residual +
+  LayerNorm (mpk_linear_residual_layernorm) and FFN + residual + next
+  LayerNorm (mpk_ffn_residual_layernorm);
+* GEMM route (wider models): per layer the QKV projection, attention, the
+  out-projection with the residual add in its epilogue (mpk_linear_residual),
+  LayerNorm (mpk_layernorm), FFN-in + GELU (mpk_linear), FFN-out + residual
+  (mpk_linear_residual) and the next LayerNorm, on large persistent GEMM tiles.
 
-plus one initial LayerNorm.  The last layer's normalized output is FP32 (it is
+The last two routes start with one LayerNorm.  The last layer's normalized output is FP32 (it is
 the model output).  Rounding points: GEMM operands FP16, accumulation / bias /
 GELU / residual / LayerNorm statistics FP32, attention probabilities FP16 only
 for the P.V product - the same points as the reference's FP16 route.
@@ -37,10 +43,10 @@ from ..custom_kernel.hip_attention import attention
 from .hip_fused import fused_layer_tail, layer_norm_qkv
 from .hip_linear import (
     layer_norm,
-    mixed_add_layer_norm,
     mixed_ffn_add_layer_norm,
     mixed_linear,
     mixed_linear_add_layer_norm,
+    mixed_linear_residual,
 )
 
 
@@ -98,8 +104,8 @@ class MixedPrecisionSelfAttention(nn.Module):
                     ctx, self.out_proj, residual_fp32, next_norm,
                     normalized_dtype=route.normalized_dtype, variant=route.out_ln_variant,
                 )
-            projected = mixed_linear(ctx, self.out_proj, output_dtype=torch.float32)
-            return mixed_add_layer_norm(residual_fp32, projected, next_norm, normalized_dtype=route.normalized_dtype)
+            x = mixed_linear_residual(ctx, self.out_proj, residual_fp32, variant=route.out_proj_variant)
+            return x, layer_norm(x, next_norm, normalized_dtype=route.normalized_dtype)
         return mixed_linear(ctx, self.out_proj, output_dtype=torch.float32)
 
 
@@ -137,8 +143,8 @@ class MixedPrecisionTransformerBlock(nn.Module):
             return mixed_linear_add_layer_norm(
                 activated, self.ffn_out, residual, next_norm, normalized_dtype=out_dtype, variant=route.out_ln_variant
             )
-        projected = mixed_linear(activated, self.ffn_out, output_dtype=torch.float32, variant=route.ffn_out_variant)
-        return mixed_add_layer_norm(residual, projected, next_norm, normalized_dtype=out_dtype)
+        x = mixed_linear_residual(activated, self.ffn_out, residual, variant=route.ffn_out_variant)
+        return x, layer_norm(x, next_norm, normalized_dtype=out_dtype)
 
 
 class MixedPrecisionTransformer(nn.Module):

@@ -1,13 +1,16 @@
 """Per-kernel timing and roofline accounting for the HIP forward.
 
 ``forward_kernel_table`` times every distinct kernel launch of one forward
-(per-operator route: initial LayerNorm, QKV projection, attention,
-out-projection + LN, FFN + LN; fused route: LayerNorm + QKV, attention, layer
-tail, last-layer tail) in isolation with HIP events recorded on the stream the kernel is launched on
+(row-fused route: initial LayerNorm, QKV projection, attention,
+out-projection + LN, FFN + LN; GEMM route: LayerNorm, QKV projection,
+attention, out-projection + residual, FFN-in + GELU, FFN-out + residual;
+layer-tail route: LayerNorm + QKV, attention, layer tail, last-layer tail) in
+isolation with HIP events recorded on the stream the kernel is launched on
 (torch's current stream, which is the stream the C ABI is given), and prices
 each against its algorithmic work:
 
 * projection ``Y = X W^T + b``:   FLOPs 2MNK;  bytes M K s_in + N K 2 + N 2 + M N s_out
+* projection + residual (FP32):   FLOPs 2MNK;  bytes M K 2 + N K 2 + N 2 + 8 M N
 * out-projection + residual + LN: FLOPs 2 M D^2; bytes M D s_in + 2 D^2 + 8 M D + M D s_norm + 16 D
 * FFN + residual + LN:            FLOPs 4 M D F; bytes M D s_in + 4 D F + M D (8 + s_norm)
 * causal attention:               FLOPs 2 B H hd S (S+1); bytes 8 B S D (fp16 q, k, v in, o out)
@@ -45,8 +48,16 @@ class KernelCost:
         return "mfma" if self.flops / PEAK_FP16_MFMA_FLOPS >= self.bytes / PEAK_HBM_BYTES else "hbm"
 
 
-def forward_costs(config, normalized_bytes: int = 2, fused_tail: bool = False) -> Dict[str, KernelCost]:
-    """Algorithmic FLOPs / bytes per launch of each kernel of one forward (one microbatch)."""
+def forward_costs(config, normalized_bytes: int = 2, route=None) -> Dict[str, KernelCost]:
+    """Algorithmic FLOPs / bytes per launch of each kernel of one forward (one microbatch).
+
+    ``route`` is a ``dispatch.Route`` (default: the route ``dispatch.plan`` picks
+    for ``config``); only the kernels that route launches are listed.
+    """
+    from . import dispatch
+
+    if route is None:
+        route = dispatch.plan(config)
     B, S, D = int(config.batch_size), int(config.seq_len), int(config.d_model)
     H, F, L = int(config.num_heads), int(config.ffn_dim), int(config.num_layers)
     M = B * S
@@ -54,7 +65,7 @@ def forward_costs(config, normalized_bytes: int = 2, fused_tail: bool = False) -
     sn = normalized_bytes
     pairs = S * (S + 1) / 2 if config.causal else S * S
     attention = KernelCost("attention", L, 4.0 * B * H * hd * pairs, 8.0 * B * S * D)
-    if fused_tail:
+    if route.fuse_layer_tail:
         w_tail = 2.0 * (D * D + 2 * D * F + 3 * D * D)
         return {
             "layernorm_qkv": KernelCost(
@@ -70,15 +81,28 @@ def forward_costs(config, normalized_bytes: int = 2, fused_tail: bool = False) -
                 M * D * (2 + 4 + 4 + 4) + 2.0 * (D * D + 2 * D * F),
             ),
         }
-    return {
-        "layernorm": KernelCost("layernorm", 1, 0.0, M * D * (4 + sn)),
+    norm_launches = 1 + (0 if route.fuse_attention_output_norm else L) + (0 if route.fuse_full_ffn else L)
+    costs = {
+        "layernorm": KernelCost("layernorm", norm_launches, 0.0, M * D * (4 + sn)),
         "qkv_proj": KernelCost("qkv_proj", L, 2.0 * M * 3 * D * D, M * D * sn + 3 * D * D * 2 + 3 * D * 2 + M * 3 * D * 2),
         "attention": attention,
-        "out_proj_ln": KernelCost(
-            "out_proj_ln", L, 2.0 * M * D * D, M * D * 2 + 2 * D * D + 8 * M * D + M * D * sn + 16 * D
-        ),
-        "ffn_ln": KernelCost("ffn_ln", L, 4.0 * M * D * F, M * D * sn + 4 * D * F + M * D * (8 + sn)),
     }
+    if route.fuse_attention_output_norm:
+        costs["out_proj_ln"] = KernelCost(
+            "out_proj_ln", L, 2.0 * M * D * D, M * D * 2 + 2 * D * D + 8 * M * D + M * D * sn + 16 * D
+        )
+    else:
+        costs["out_proj_residual"] = KernelCost(
+            "out_proj_residual", L, 2.0 * M * D * D, M * D * 2 + 2 * D * D + 2 * D + 8 * M * D
+        )
+    if route.fuse_full_ffn:
+        costs["ffn_ln"] = KernelCost("ffn_ln", L, 4.0 * M * D * F, M * D * sn + 4 * D * F + M * D * (8 + sn))
+    else:
+        costs["ffn_in"] = KernelCost("ffn_in", L, 2.0 * M * D * F, M * D * sn + 2 * D * F + 2 * F + M * F * 2)
+        costs["ffn_out_residual"] = KernelCost(
+            "ffn_out_residual", L, 2.0 * M * D * F, M * F * 2 + 2 * D * F + 2 * D + 8 * M * D
+        )
+    return costs
 
 
 def time_launches(fn: Callable[[], object], iterations: int, warmup: int = 3) -> float:
@@ -135,7 +159,9 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
     """Time each distinct kernel of ``model``'s forward on input ``x`` (first layer's weights)."""
     from .custom_kernel.hip_attention import attention
     from .mixed_precision.hip_fused import fused_layer_tail, layer_norm_qkv
-    from .mixed_precision.hip_linear import layer_norm, mixed_ffn_add_layer_norm, mixed_linear, mixed_linear_add_layer_norm
+    from .mixed_precision.hip_linear import (
+        layer_norm, mixed_ffn_add_layer_norm, mixed_linear, mixed_linear_add_layer_norm, mixed_linear_residual,
+    )
 
     import dataclasses
 
@@ -147,7 +173,7 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
     config = dataclasses.replace(model.config, batch_size=B) if dataclasses.is_dataclass(model.config) else model.config
     sdt = route.normalized_dtype
     causal = bool(config.causal)
-    costs = forward_costs(config, 2 if sdt == torch.float16 else 4, route.fuse_layer_tail)
+    costs = forward_costs(config, 2 if sdt == torch.float16 else 4, route)
     with torch.inference_mode():
         if route.fuse_layer_tail:
             qkv = layer_norm_qkv(x, layer.norm1, att.qkv_proj, variant=route.head_variant)
@@ -167,8 +193,14 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
             qkv = mixed_linear(normalized, att.qkv_proj, output_dtype=torch.float16, variant=route.qkv_variant)
             q, k, v = qkv.view(B, S, 3, att.num_heads, att.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
             ctx = attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant).view(B, S, D)
-            resid, nffn = mixed_linear_add_layer_norm(ctx, att.out_proj, x, layer.norm2, normalized_dtype=sdt,
-                                                      variant=route.out_ln_variant)
+            if route.fuse_attention_output_norm:
+                resid, nffn = mixed_linear_add_layer_norm(ctx, att.out_proj, x, layer.norm2, normalized_dtype=sdt,
+                                                          variant=route.out_ln_variant)
+            else:
+                resid = mixed_linear_residual(ctx, att.out_proj, x, variant=route.out_proj_variant)
+                nffn = layer_norm(resid, layer.norm2, normalized_dtype=sdt)
+            hidden = mixed_linear(nffn, layer.ffn_in, output_dtype=torch.float16, fuse_gelu=True,
+                                  variant=route.ffn_in_variant)
             launches = {
                 "layernorm": lambda: layer_norm(x, layer.norm1, normalized_dtype=sdt),
                 "qkv_proj": lambda: mixed_linear(normalized, att.qkv_proj, output_dtype=torch.float16,
@@ -176,21 +208,27 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
                 "attention": lambda: attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant),
                 "out_proj_ln": lambda: mixed_linear_add_layer_norm(ctx, att.out_proj, x, layer.norm2,
                                                                    normalized_dtype=sdt, variant=route.out_ln_variant),
+                "out_proj_residual": lambda: mixed_linear_residual(ctx, att.out_proj, x,
+                                                                   variant=route.out_proj_variant),
                 "ffn_ln": lambda: mixed_ffn_add_layer_norm(nffn, layer.ffn_in, layer.ffn_out, resid, layer.norm1,
                                                            normalized_dtype=sdt, variant=route.ffn_variant),
+                "ffn_in": lambda: mixed_linear(nffn, layer.ffn_in, output_dtype=torch.float16, fuse_gelu=True,
+                                               variant=route.ffn_in_variant),
+                "ffn_out_residual": lambda: mixed_linear_residual(hidden, layer.ffn_out, resid,
+                                                                  variant=route.ffn_out_variant),
             }
         rows = []
         for name, fn in launches.items():
-            if costs[name].launches_per_forward == 0:
+            if name not in costs or costs[name].launches_per_forward == 0:
                 continue
             rows.append(_row(name, costs[name], time_launches(fn, iterations)))
     return rows
 
 
-def forward_roofline_seconds(config, microbatches: int = 1, fused_tail: bool = False) -> float:
+def forward_roofline_seconds(config, microbatches: int = 1, route=None) -> float:
     """Lower bound on one forward: sum over kernels of max(FLOPs/MFMA peak, bytes/HBM peak)."""
     total = 0.0
-    for cost in forward_costs(config, 2, fused_tail).values():
+    for cost in forward_costs(config, 2, route).values():
         total += cost.launches_per_forward * max(cost.flops / PEAK_FP16_MFMA_FLOPS, cost.bytes / PEAK_HBM_BYTES)
     return total * microbatches
 
