@@ -7,8 +7,11 @@
 // Math per query row (same rounding points as the FP16 reference kernel):
 //   s_j*c = (q*c) . k_j  (FP16 operands: q*c split into hi + lo; FP32 accumulate)
 //   m   = running max of s*c (FP32, raised lazily);  p_j = 2^(s_j*c - m), c = scale*log2(e)
-//   l   = running sum of p_j in FP32;  acc += fp16(p_j) * v_j  (FP32 accumulate)
+//   acc += fp16(p_j) * v_j  and  l += fp16(p_j)  (both by the PV MFMA, FP32 accumulate)
 //   o   = acc / l, rounded to the output type.
+// l sums the same FP16-rounded probabilities that weight V (the reference sums the
+// unrounded FP32 p_j); the two sums differ by at most 2^-12 relative (half an FP16
+// ulp of o), and this way the weights applied to V sum to exactly one.
 // For FP32 inputs (the reference's TF32 kernel) q, k, v are rounded to FP16 on
 // load, which keeps the same 10-bit operand mantissa as TF32.
 //
@@ -140,14 +143,20 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
   // ---- running statistics (log2 units) and output accumulators ----
   // mrow: running max of s*c for the query row; fresh: the row has not seen a
   // visible key yet (its tiles are computed without the -mrow offset).
-  float mrow[QT], l_run[QT];
+  float mrow[QT];
   bool fresh[QT];
   f4 oacc[QT][SH::DT][2];
+  // Row sums of fp16(P) come out of the PV product: an extra A operand whose
+  // row 0 is all ones gives sum_k P[q][k] in row 0 of lsum (lanes of group 0).
+  f4 lsum_acc[QT];
+  h8 ones_row;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones_row[j] = r == 0 ? (_Float16)1.0f : (_Float16)0.0f;
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     mrow[t] = 0.f;
     fresh[t] = true;
-    l_run[t] = 0.f;
+    lsum_acc[t] = zero4();
 #pragma unroll
     for (int dt = 0; dt < SH::DT; ++dt) oacc[t][dt][0] = oacc[t][dt][1] = zero4();
   }
@@ -290,7 +299,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
         const float shift = shift_row ? mx : 0.f;
         if (shift_row && !fresh[t]) {
           const float alpha = __builtin_amdgcn_exp2f(-shift);
-          l_run[t] *= alpha;
+          lsum_acc[t] *= alpha;
 #pragma unroll
           for (int dt = 0; dt < SH::DT; ++dt) {
             oacc[t][dt][0] *= alpha;
@@ -308,23 +317,19 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) sc[p][tt][t][i] -= shift;
       }
-      float psum = 0.f;
 #pragma unroll
       for (int p = 0; p < NP; ++p)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float pv = __builtin_amdgcn_exp2f(sc[p][tt][t][i]);
-            psum += pv;
-            pf[t][p][4 * tt + i] = (_Float16)pv;
-          }
-      l_run[t] += psum;
+          for (int i = 0; i < 4; ++i) pf[t][p][4 * tt + i] = (_Float16)__builtin_amdgcn_exp2f(sc[p][tt][t][i]);
     }
 
-    // O^T += V^T P^T
+    // O^T += V^T P^T, and the row sums of P
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
+#pragma unroll
+      for (int t = 0; t < QT; ++t) lsum_acc[t] = mfma32(ones_row, pf[t][p], lsum_acc[t]);
       if constexpr (HD == 16) {
         const h8 va = *reinterpret_cast<const h8*>(&vtb[r * SH::LDV + 32 * p + 8 * g]);
 #pragma unroll
@@ -362,7 +367,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     const int q = qw0 + 16 * t + r;
-    const float lsum = sum_over_groups(l_run[t]);
+    const float lsum = sum_over_groups(lsum_acc[t][0]);
     const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
     if (q >= S) continue;
     OT* dst = O + (int64_t)q * a.os[2];
