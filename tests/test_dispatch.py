@@ -29,7 +29,11 @@ def test_enable_flags_change_the_route():
     assert r.normalized_dtype == torch.float32 and not r.fuse_layer_tail
 
 
-@pytest.mark.parametrize("d,h,ok", [(128, 4, True), (96, 3, True), (128, 16, False), (24, 3, False), (40, 5, False)])
+@pytest.mark.parametrize(
+    "d,h,ok",
+    [(128, 4, True), (96, 3, True), (128, 16, True), (24, 3, True), (1024, 4, True), (96, 2, False), (36, 3, False),
+     (512, 1, False)],
+)
 def test_support_limits(d, h, ok):
     route = dispatch.plan(TransformerConfig(2, 8, d, h, 64, 1, True))
     assert route.supported == ok

@@ -266,7 +266,7 @@ def _packed_qkv(b, s, h, hd, seed, device, dtype):
 @pytest.mark.parametrize(
     "b,h,s,hd",
     [(2, 4, 128, 32), (2, 2, 256, 16), (1, 8, 300, 64), (1, 2, 77, 128), (3, 4, 1024, 32), (1, 1, 1, 32),
-     (2, 3, 65, 16), (1, 2, 2048, 64)],
+     (2, 3, 65, 16), (1, 2, 2048, 64), (2, 16, 128, 8), (1, 4, 333, 8), (2, 4, 128, 256), (1, 2, 517, 256)],
 )
 @pytest.mark.parametrize("variant", [1, 2])
 def test_fp16_causal_attention(hip_device, b, h, s, hd, variant):
@@ -284,7 +284,7 @@ def test_fp16_causal_attention(hip_device, b, h, s, hd, variant):
         _close(fp16_causal_attention(q, k, v, scale), ref, 3e-3, 3e-3, "fp16_causal_attention")
 
 
-@pytest.mark.parametrize("b,h,s,hd", [(2, 4, 128, 32), (1, 2, 200, 64), (2, 2, 96, 16)])
+@pytest.mark.parametrize("b,h,s,hd", [(2, 4, 128, 32), (1, 2, 200, 64), (2, 2, 96, 16), (2, 4, 70, 8), (1, 2, 90, 256)])
 def test_attention_noncausal_fp32io_and_keymask(hip_device, b, h, s, hd):
     from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention, causal_attention
 

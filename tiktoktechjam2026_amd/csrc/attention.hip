@@ -46,17 +46,20 @@ struct AttnArgs {
 
 template <int HD, int KTILE, int NT>
 struct AttnShape {
-  static constexpr int LDK = HD + 8;      // K tile row stride (halves)
+  // HP: the head dim the MFMA tiles see.  hd = 8 runs on the hd = 16 tiles with
+  // dims 8..15 of K zero (Q's are zero too) and V^T rows 8..15 never stored.
+  static constexpr int HP = HD < 16 ? 16 : HD;
+  static constexpr int LDK = HP + 8;      // K tile row stride (halves)
   static constexpr int LDV = KTILE + 8;   // V^T tile row stride (halves)
   static constexpr int CPK = HD / 8;      // 8-element chunks per key row
   static constexpr int CHUNKS = KTILE * CPK;                     // K tile: one 16-byte chunk per item
   static constexpr int PER_THREAD = (CHUNKS + NT - 1) / NT;
   static constexpr int VITEMS = (KTILE / 2) * CPK;               // V tile: a key pair x one chunk per item
   static constexpr int V_PER_THREAD = (VITEMS + NT - 1) / NT;
-  static constexpr int DT = HD >= 32 ? HD / 32 : 1;  // output d tiles (pairs of 16, or one tile of 16)
+  static constexpr int DT = HP >= 32 ? HP / 32 : 1;  // output d tiles (pairs of 16, or one tile of 16)
   static constexpr int NP = KTILE / 32;              // key pairs per tile
   static constexpr int KBUF = KTILE * LDK;
-  static constexpr int VBUF = HD * LDV;
+  static constexpr int VBUF = HP * LDV;
 };
 
 template <int HD, int QT, int KTILE, int NW, typename IT, typename OT, bool KEYMASK>
@@ -65,7 +68,8 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
   using SH = AttnShape<HD, KTILE, NT>;
   constexpr int QB = 16 * QT * NW;
   constexpr int NP = SH::NP;
-  static_assert(HD == 16 || HD == 32 || HD == 64 || HD == 128, "head dim");
+  constexpr int HP = SH::HP;
+  static_assert(HD == 8 || HD == 16 || HD == 32 || HD == 64 || HD == 128 || HD == 256, "head dim");
   static_assert(KTILE % 32 == 0 && KTILE <= NT, "key tile");
 
   __shared__ _Float16 ks_lds[2][SH::KBUF];
@@ -108,15 +112,15 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
   // (hi + lo = q*c to ~2^-22 relative), so two MFMAs give s*c - m directly in
   // the FP32 accumulator (which starts at -m): no per-score scaling FMA, and the
   // exponent argument is more accurate than rounding s*c separately.
-  constexpr int QK_STEPS = HD >= 32 ? HD / 32 : 1;
+  constexpr int QK_STEPS = HP >= 32 ? HP / 32 : 1;
   h8 qh[QT][QK_STEPS], ql[QT][QK_STEPS];
   h4 qh16[QT], ql16[QT];
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     const int q = qw0 + 16 * t + r;
-    if constexpr (HD == 16) {
+    if constexpr (HP == 16) {
       float v[4] = {0.f, 0.f, 0.f, 0.f};
-      if (q < S) {
+      if (q < S && 4 * g < HD) {
         const IT* src = Q + (int64_t)q * a.qs[2] + 4 * g;
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = (float)(_Float16)src[j] * a.c;
@@ -240,7 +244,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
           const float c0 = fresh[t] ? 0.f : -mrow[t];
           sc[p][tt][t] = f4{c0, c0, c0, c0};
         }
-        if constexpr (HD == 16) {
+        if constexpr (HP == 16) {
           const h4 ka = *reinterpret_cast<const h4*>(&ksb[krow * SH::LDK + 4 * g]);
 #pragma unroll
           for (int t = 0; t < QT; ++t) {
@@ -330,7 +334,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
     for (int p = 0; p < NP; ++p) {
 #pragma unroll
       for (int t = 0; t < QT; ++t) lsum_acc[t] = mfma32(ones_row, pf[t][p], lsum_acc[t]);
-      if constexpr (HD == 16) {
+      if constexpr (HP == 16) {
         const h8 va = *reinterpret_cast<const h8*>(&vtb[r * SH::LDV + 32 * p + 8 * g]);
 #pragma unroll
         for (int t = 0; t < QT; ++t) oacc[t][0][0] = mfma32(va, pf[t][p], oacc[t][0][0]);
@@ -351,6 +355,12 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
   // Double-buffered pipeline, one barrier per tile: tile i+1 is fetched into
   // registers while tile i is processed, then staged into the other buffer
   // (last read in iteration i-1, which every wave left before the barrier).
+  if constexpr (HD < HP) {
+    // the padding dims are never staged: zero them once (K's feed the QK^T sums)
+    for (int i = threadIdx.x; i < 2 * SH::KBUF; i += NT) (&ks_lds[0][0])[i] = (_Float16)0.0f;
+    for (int i = threadIdx.x; i < 2 * SH::VBUF; i += NT) (&vt_lds[0][0])[i] = (_Float16)0.0f;
+    __syncthreads();
+  }
   fetch(0);
   stash(0);
   __syncthreads();
@@ -371,10 +381,12 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
     const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
     if (q >= S) continue;
     OT* dst = O + (int64_t)q * a.os[2];
-    if constexpr (HD == 16) {
+    if constexpr (HP == 16) {
       // lane group g holds d = 4g .. 4g+3
+      if (4 * g < HD) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dst[4 * g + i] = (OT)(oacc[t][0][0][i] * inv);
+        for (int i = 0; i < 4; ++i) dst[4 * g + i] = (OT)(oacc[t][0][0][i] * inv);
+      }
     } else {
 #pragma unroll
       for (int dt = 0; dt < SH::DT; ++dt) {
@@ -419,13 +431,24 @@ static hipError_t attn_variant(int variant, const AttnArgs& a, hipStream_t s) {
   }
 }
 
+// hd = 256: one tile shape (16 queries/wave, 32-key tiles, 4 waves), whatever the
+// variant id - the K and V^T tiles of larger shapes do not leave room in LDS and
+// registers for more than one workgroup per CU.
+template <typename IT, typename OT>
+static hipError_t attn_variant_256(int variant, const AttnArgs& a, hipStream_t s) {
+  if (variant < 1 || variant > 5) return (hipError_t)MPK_EUNSUPPORTED;
+  return launch_attn<256, 1, 32, 4, IT, OT>(a, s);
+}
+
 template <typename IT, typename OT>
 static hipError_t attn_dispatch(int variant, const AttnArgs& a, int hd, hipStream_t s) {
   switch (hd) {
+    case 8: return attn_variant<8, IT, OT>(variant, a, s);
     case 16: return attn_variant<16, IT, OT>(variant, a, s);
     case 32: return attn_variant<32, IT, OT>(variant, a, s);
     case 64: return attn_variant<64, IT, OT>(variant, a, s);
     case 128: return attn_variant<128, IT, OT>(variant, a, s);
+    case 256: return attn_variant_256<IT, OT>(variant, a, s);
     default: return (hipError_t)MPK_EUNSUPPORTED;
   }
 }
@@ -450,7 +473,8 @@ extern "C" int mpk_causal_attention(const void* q, const void* k, const void* v,
   if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return MPK_EINVAL;
   if (batch < 0 || heads <= 0 || seq_len < 0) return MPK_EINVAL;
   if ((io_dtype != kF32 && io_dtype != kF16) || (out_dtype != kF32 && out_dtype != kF16)) return MPK_EINVAL;
-  if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128) return MPK_EUNSUPPORTED;
+  if (head_dim != 8 && head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return MPK_EUNSUPPORTED;
   const int64_t* st[4] = {q_strides, k_strides, v_strides, o_strides};
   const void* base[4] = {q, k, v, o};
   for (int i = 0; i < 4; ++i) {

@@ -10,7 +10,7 @@ head_dim]`` tensor, which is the ``[tokens, d_model]`` layout the output
 projection reads without a transpose.
 
 Differences from the reference, all widening: any sequence length (the
-reference accepts 128 and 1024 only), head_dim in {16, 32, 64, 128}, an
+reference accepts 128 and 1024 only), head_dim in {8, 16, 32, 64, 128, 256}, an
 optional key-padding mask, and FP32 inputs handled by the same FP16-MFMA kernel
 (operands rounded to FP16, i.e. the same 10-bit mantissa the reference's TF32
 dots use).
@@ -25,7 +25,7 @@ import torch
 
 from .. import _lib
 
-HEAD_DIMS = (16, 32, 64, 128)
+HEAD_DIMS = (8, 16, 32, 64, 128, 256)
 
 
 def _common_ok(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dtype: torch.dtype) -> bool:

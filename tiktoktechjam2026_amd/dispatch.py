@@ -39,7 +39,7 @@ from typing import Dict, Tuple
 import torch
 
 LN_FUSED_WIDTHS = (32, 64, 128, 256, 512)
-ATTENTION_HEAD_DIMS = (16, 32, 64, 128)
+ATTENTION_HEAD_DIMS = (8, 16, 32, 64, 128, 256)
 # (d_model, ffn_dim) pairs built into the whole-layer tail kernel (its weights fit in LDS);
 # must equal mpk_layer_tail_supported / mpk_layernorm_qkv_supported in the library.
 LAYER_TAIL_SHAPES = frozenset({(32, 32), (32, 64), (32, 128), (64, 64), (64, 128), (64, 256), (128, 128)})
