@@ -175,22 +175,29 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
   // instruction - no bank conflicts, and a quarter of the 16-bit stores.
   h8 kreg[SH::PER_THREAD], vreg[SH::V_PER_THREAD][2];
   float breg = 0.f;
+  // Buffer resources cover only the tile's keys that exist (min(KTILE, S - kb)
+  // rows), so the hardware returns zeros for keys past the end of the sequence.
+  const uint32_t krow_bytes = (uint32_t)(a.ks[2] * (int64_t)sizeof(IT));
+  const uint32_t vrow_bytes = (uint32_t)(a.vs[2] * (int64_t)sizeof(IT));
   auto fetch = [&](int kb) {
+    const uint32_t rows = (uint32_t)min(KTILE, S - kb);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(Kp + (int64_t)kb * a.ks[2], rows * krow_bytes);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(Vp + (int64_t)kb * a.vs[2], rows * vrow_bytes);
 #pragma unroll
     for (int i = 0; i < SH::PER_THREAD; ++i) {
       const int c = threadIdx.x + i * NT;
       const int key = c / SH::CPK, col = (c % SH::CPK) * 8;
-      const int gk = kb + key;
-      kreg[i] = c < SH::CHUNKS && gk < S ? load8_as_half(Kp + (int64_t)gk * a.ks[2] + col) : zero_h8();
+      if (c < SH::CHUNKS) kreg[i] = buffer_load8_as_half(kr, key * krow_bytes + col * (uint32_t)sizeof(IT), Kp);
     }
 #pragma unroll
     for (int i = 0; i < SH::V_PER_THREAD; ++i) {
       const int c = threadIdx.x + i * NT;
       const int kp = c % (KTILE / 2), col = (c / (KTILE / 2)) * 8;
-      const int gk = kb + 2 * kp;
-      const bool ok = c < SH::VITEMS;
-      vreg[i][0] = ok && gk < S ? load8_as_half(Vp + (int64_t)gk * a.vs[2] + col) : zero_h8();
-      vreg[i][1] = ok && gk + 1 < S ? load8_as_half(Vp + (int64_t)(gk + 1) * a.vs[2] + col) : zero_h8();
+      if (c < SH::VITEMS) {
+        const uint32_t off = 2 * kp * vrow_bytes + col * (uint32_t)sizeof(IT);
+        vreg[i][0] = buffer_load8_as_half(vr, off, Vp);
+        vreg[i][1] = buffer_load8_as_half(vr, off + vrow_bytes, Vp);
+      }
     }
     if (threadIdx.x < KTILE) {
       const int gk = kb + threadIdx.x;

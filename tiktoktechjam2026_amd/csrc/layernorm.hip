@@ -44,7 +44,14 @@ __global__ __launch_bounds__(kBlock) void residual_layernorm_kernel(
       const int c = lane + v * G;
       float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
       if (row < rows && c < nvec) {
-        a = reinterpret_cast<const float4*>(x + row * d)[c];
+        if constexpr (HAS_U) {
+          a = reinterpret_cast<const float4*>(x + row * d)[c];
+        } else {
+          // plain LayerNorm: x is read once and n written once, so both bypass
+          // the caches (non-temporal); measured ~10% faster on MI355X
+          const f4 t = __builtin_nontemporal_load(reinterpret_cast<const f4*>(x + row * d) + c);
+          a = make_float4(t[0], t[1], t[2], t[3]);
+        }
         if (HAS_U) {
           const float4 b = reinterpret_cast<const float4*>(u + row * d)[c];
           a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
@@ -85,11 +92,14 @@ __global__ __launch_bounds__(kBlock) void residual_layernorm_kernel(
         o[3] = (r[k][v].w - mean) * rstd * gm.w + bt.w;
         OT* dst = norm_out + row * d + 4 * c;
         if constexpr (sizeof(OT) == 4) {
-          *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+          const f4 v = {o[0], o[1], o[2], o[3]};
+          if constexpr (HAS_U) *reinterpret_cast<f4*>(dst) = v;
+          else __builtin_nontemporal_store(v, reinterpret_cast<f4*>(dst));
         } else {
           h4 h;
           h[0] = (_Float16)o[0]; h[1] = (_Float16)o[1]; h[2] = (_Float16)o[2]; h[3] = (_Float16)o[3];
-          *reinterpret_cast<h4*>(dst) = h;
+          if constexpr (HAS_U) *reinterpret_cast<h4*>(dst) = h;
+          else __builtin_nontemporal_store(h, reinterpret_cast<h4*>(dst));
         }
       }
     }

@@ -277,25 +277,33 @@ __global__ __launch_bounds__(2 * BN) void linear_big_kernel(LinearArgs a) {
 #pragma unroll
       for (int t = 0; t < TM; ++t) acc[p][tt][t] = zero4();
 
+  // Tile loads go through buffer resources that cover only the tile's existing
+  // rows: rows past M (or N) read as zeros without per-lane predication.  Only a
+  // partial last K chunk (K % 64 != 0) masks columns per lane.
   h8 xr[XCH], wr[WCH];
+  const uint32_t xrow_bytes = (uint32_t)K * (uint32_t)sizeof(XT);
+  const uint32_t wrow_bytes = (uint32_t)K * 2u;
   auto fetch = [&](int ftile, int k0) {
     const int64_t fm0 = (int64_t)(ftile / nbn) * BM;
     const int fn0 = (ftile % nbn) * BN;
+    const uint32_t xrows = (uint32_t)min<int64_t>(BM, M - fm0);
+    const uint32_t wrows = (uint32_t)min(BN, N - fn0);
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(X + fm0 * K, xrows * xrow_bytes);
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W + (int64_t)fn0 * K, wrows * wrow_bytes);
+    const bool full_k = k0 + BK <= K;
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
       const int c = threadIdx.x + i * NT;
       const int row = c / CPR, col = (c % CPR) * 8;
-      const int64_t gm = fm0 + row;
-      const int gk = k0 + col;
-      xr[i] = gm < M && gk < K ? load8_as_half(X + gm * K + gk) : zero_h8();
+      const uint32_t off = row * xrow_bytes + (uint32_t)(k0 + col) * (uint32_t)sizeof(XT);
+      xr[i] = full_k || k0 + col < K ? buffer_load8_as_half(xrs, off, X) : zero_h8();
     }
 #pragma unroll
     for (int i = 0; i < WCH; ++i) {
       const int c = threadIdx.x + i * NT;
       const int row = c / CPR, col = (c % CPR) * 8;
-      const int gn = fn0 + row;
-      const int gk = k0 + col;
-      wr[i] = gn < N && gk < K ? load8_as_half(W + (int64_t)gn * K + gk) : zero_h8();
+      const uint32_t off = row * wrow_bytes + (uint32_t)(k0 + col) * 2u;
+      wr[i] = full_k || k0 + col < K ? buffer_load8_as_half(wrs, off, W) : zero_h8();
     }
   };
   auto stash = [&](int buf) {
@@ -424,6 +432,7 @@ static int resident_grid(Kernel kernel, int threads, size_t lds) {
 
 template <int BN, int STAGES, typename XT, int EPI, typename OT>
 static hipError_t launch_linear_big(const LinearArgs& a, hipStream_t s) {
+  if (a.k > (1 << 20)) return (hipError_t)MPK_EUNSUPPORTED;  // 32-bit tile offsets: 256 rows x K x 4 bytes
   const int64_t tiles = ((a.m + 255) / 256) * ((a.n + BN - 1) / BN);
   if (tiles > 0x7fffffff) return hipErrorInvalidConfiguration;
   auto kernel = linear_big_kernel<BN, STAGES, XT, EPI, OT>;
@@ -493,7 +502,7 @@ using namespace mpk;
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 extern "C" int mpk_linear_auto_variant(int64_t m, int32_t n, int32_t k) {
-  if (n % 256 == 0 && k >= 256 && ((m + 255) / 256) * (n / 256) >= 256) return 7;
+  if (n % 256 == 0 && k >= 256 && k <= (1 << 20) && ((m + 255) / 256) * (n / 256) >= 256) return 7;
   if (n % 128 == 0 && m >= 128 * 256) return 1;
   if (n % 128 == 0) return 4;
   if (n % 64 == 0) return 2;

@@ -64,6 +64,33 @@ __device__ __forceinline__ h8 load8_as_half(const float* p) {
   return r;
 }
 
+// Hardware bounds-checked loads.  A raw buffer resource over [base, base + bytes)
+// returns zeros for a 16-byte chunk that starts at or past `bytes`, so tile loads
+// that run off the end of a sequence need no per-lane predication or zero fill.
+// (0x00020000: the gfx9 buffer format word for 32-bit untyped data.)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ h8 buffer_load8_as_half(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, const _Float16*) {
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  const u4 v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+  return __builtin_bit_cast(h8, v);
+}
+
+__device__ __forceinline__ h8 buffer_load8_as_half(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, const float*) {
+  typedef float v4 __attribute__((ext_vector_type(4)));
+  const v4 a = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+  const v4 b = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off + 16, 0, 0));
+  h8 h;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    h[j] = (_Float16)a[j];
+    h[4 + j] = (_Float16)b[j];
+  }
+  return h;
+}
+
 __device__ __forceinline__ h8 zero_h8() {
   h8 r;
 #pragma unroll
