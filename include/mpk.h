@@ -107,7 +107,9 @@ int mpk_ffn_residual_layernorm_auto_variant(int64_t m, int32_t d, int32_t f);
  * (strides in elements: batch, head, seq, dim; dim stride must be 1);
  * o: same indexing in out_dtype.  key_valid: optional [batch, seq_len] bytes,
  * nonzero = key may be attended (NULL = all valid).  scale multiplies q.k.
- * head_dim in {16, 32, 64, 128}.
+ * head_dim in {8, 16, 32, 64, 128, 256}.  variant: 0 = built-in choice
+ * (mpk_attention_auto_variant), 1..5 tile shapes of the 16x16-MFMA kernel,
+ * 6..8 the 32x32-MFMA kernel (head_dim 32 and 64 only, else MPK_EUNSUPPORTED).
  * Replaces: fp16_causal_attention (custom_kernel/triton_attention.py:341-390)
  *           and causal_attention (custom_kernel/triton_attention.py:320-338).
  */

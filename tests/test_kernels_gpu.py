@@ -268,7 +268,7 @@ def _packed_qkv(b, s, h, hd, seed, device, dtype):
     [(2, 4, 128, 32), (2, 2, 256, 16), (1, 8, 300, 64), (1, 2, 77, 128), (3, 4, 1024, 32), (1, 1, 1, 32),
      (2, 3, 65, 16), (1, 2, 2048, 64), (2, 16, 128, 8), (1, 4, 333, 8), (2, 4, 128, 256), (1, 2, 517, 256)],
 )
-@pytest.mark.parametrize("variant", [1, 2])
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5])
 def test_fp16_causal_attention(hip_device, b, h, s, hd, variant):
     from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention, fp16_causal_attention, is_fp16_supported
 
@@ -282,6 +282,52 @@ def test_fp16_causal_attention(hip_device, b, h, s, hd, variant):
     _close(out, ref, 3e-3, 3e-3, "fp16 causal attention")
     if variant == 1:
         _close(fp16_causal_attention(q, k, v, scale), ref, 3e-3, 3e-3, "fp16_causal_attention")
+
+
+@pytest.mark.parametrize(
+    "b,h,s,hd",
+    [(2, 4, 128, 32), (1, 8, 300, 64), (3, 4, 1024, 32), (1, 1, 1, 32), (2, 3, 65, 64), (1, 2, 2048, 64),
+     (1, 2, 4096, 32), (2, 2, 33, 32), (1, 3, 517, 64)],
+)
+@pytest.mark.parametrize("variant", [6, 7, 8])
+def test_fp16_causal_attention_32x32(hip_device, b, h, s, hd, variant):
+    """The 32x32-MFMA kernel (head_dim 32 / 64) against the float64 reference."""
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention
+
+    _, q, k, v = _packed_qkv(b, s, h, hd, 47, hip_device, torch.float16)
+    scale = hd ** -0.5
+    out = attention(q, k, v, scale, causal=True, variant=variant)
+    assert out.shape == (b, s, h, hd) and out.dtype == torch.float16 and out.is_contiguous()
+    _close(out, _ref_attention(q, k, v, scale, True), 3e-3, 3e-3, "fp16 causal attention (32x32)")
+
+
+@pytest.mark.parametrize("variant", [6, 7, 8])
+def test_attention_32x32_noncausal_fp32io_keymask_negative_scale(hip_device, variant):
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention
+
+    for b, h, s, hd in ((2, 4, 130, 32), (1, 2, 200, 64)):
+        _, q, k, v = _packed_qkv(b, s, h, hd, 53, hip_device, torch.float32)
+        scale = hd ** -0.5
+        out = attention(q, k, v, scale, causal=False, variant=variant)
+        assert out.dtype == torch.float32
+        _close(out, _ref_attention(q, k, v, scale, False), 3e-3, 3e-3, "non-causal fp32 io (32x32)")
+        out_n = attention(q.half(), k.half(), v.half(), -scale, causal=True, variant=variant)
+        _close(out_n, _ref_attention(q, k, v, -scale, True), 3e-3, 3e-3, "negative scale (32x32)")
+        lengths = torch.tensor([max(1, s - 37 * (i + 1)) for i in range(b)])
+        key_valid = (torch.arange(s)[None, :] < lengths[:, None]).to(hip_device)
+        key_valid[:, 0] = False  # the first key masked: rows see their first valid key in a later tile
+        out_m = attention(q.half(), k.half(), v.half(), scale, causal=True, key_valid=key_valid, variant=variant)
+        ref_m = _ref_attention(q, k, v, scale, True, key_valid)
+        rows_with_keys = torch.isfinite(ref_m).all(dim=-1)
+        _close(out_m.cpu()[rows_with_keys], ref_m[rows_with_keys], 3e-3, 3e-3, "key mask (32x32)")
+
+
+def test_attention_32x32_rejects_other_head_dims(hip_device):
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention
+
+    _, q, k, v = _packed_qkv(1, 64, 2, 16, 59, hip_device, torch.float16)
+    with pytest.raises(RuntimeError):
+        attention(q, k, v, 0.25, causal=True, variant=6)
 
 
 @pytest.mark.parametrize("b,h,s,hd", [(2, 4, 128, 32), (1, 2, 200, 64), (2, 2, 96, 16), (2, 4, 70, 8), (1, 2, 90, 256)])

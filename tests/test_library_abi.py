@@ -86,7 +86,11 @@ def test_auto_variant_queries(built_library):
     assert lib.mpk_linear_auto_variant(65536, 384, 128) in (1, 2, 3, 4)
     assert lib.mpk_linear_residual_layernorm_auto_variant(65536, 128) in (1, 2)
     assert lib.mpk_ffn_residual_layernorm_auto_variant(65536, 128, 128) in (1, 2)
-    assert lib.mpk_attention_auto_variant(64, 4, 1024, 32) in (1, 2)
+    assert lib.mpk_attention_auto_variant(64, 4, 1024, 32) in range(1, 9)
+    # the 32x32 kernel variants (6..8) only for head_dim 32 / 64
+    for hd in (8, 16, 128, 256):
+        for s in (128, 1024, 4096):
+            assert lib.mpk_attention_auto_variant(4, 4, s, hd) in range(1, 6)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -42,6 +42,12 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source additions.  The attention kernel never produces NaN from finite
+# inputs (masked scores are -inf, exp2(-inf) = 0), so its max reductions need
+# no NaN canonicalisation.
+EXTRA_FLAGS = {"attention.hip": ["-fno-honor-nans"]}
+
+
 def _hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(path):
@@ -55,7 +61,7 @@ def sources() -> List[str]:
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [_hipcc(), *COMMON_FLAGS, "-c", src, "-o", obj]
+    cmd = [_hipcc(), *COMMON_FLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {os.path.basename(src)}:\n{proc.stdout}")

@@ -26,6 +26,8 @@
 // tiles that straddle the diagonal (or the sequence end, or carry a key mask)
 // pay for masking.  Query blocks are issued longest first, and each XCD owns a
 // contiguous range of (batch, head) rows so they share K/V through its L2.
+#include <type_traits>
+
 #include "mpk_common.h"
 
 namespace mpk {
@@ -234,21 +236,31 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
   };
 
   // ---- one key tile: S^T, online softmax, O^T += V^T P^T ----
-  auto process = [&](const int kb, const _Float16* ksb, const _Float16* vtb, const float* kbb) {
+  // FIRST: the tile may hold a row's first visible key, so rows can still be
+  // "fresh" (their scores were computed without the -mrow offset).  Without a
+  // key mask every row sees key 0, so only tile 0 needs that handling and the
+  // steady-state tiles skip it.
+  auto process = [&](const int kb, const _Float16* ksb, const _Float16* vtb, const float* kbb, auto first_tag) {
+    constexpr bool MAYBE_FRESH = decltype(first_tag)::value || KEYMASK;
     if (a.causal && kb > qw_last) return;  // whole tile is in this wave's future
-    const bool need_causal = a.causal && kb + KTILE - 1 > qw0;  // tile straddles this wave's diagonal
-    const bool need_bias = KEYMASK || kb + KTILE > S;          // padded keys or keys past the end
+    // Key pairs [0, npv) hold keys visible to some query of this wave; in a
+    // causal tile on the diagonal only the last of them straddles it (queries of
+    // a wave are 16-aligned, pairs 32-aligned) and the pairs after it are skipped.
+    const int npv = a.causal ? min(NP, (qw_last - kb) / 32 + 1) : NP;
+    const bool need_causal = a.causal && kb + 32 * npv - 1 > qw0;  // last visible pair straddles the diagonal
+    const bool need_bias = KEYMASK || kb + KTILE > S;               // padded keys or keys past the end
 
-    // S^T = K (Q*c)^T - m for KTILE keys x 16*QT queries
+    // S^T = K (Q*c)^T - m for the visible key pairs x 16*QT queries
     f4 sc[NP][2][QT];  // [key pair][tile in pair][q tile]
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
+    for (int p = 0; p < NP; ++p) {
+      if (p >= npv) break;
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         const int krow = 32 * p + pair_row(r, tt);
 #pragma unroll
         for (int t = 0; t < QT; ++t) {
-          const float c0 = fresh[t] ? 0.f : -mrow[t];
+          const float c0 = (MAYBE_FRESH && fresh[t]) ? 0.f : -mrow[t];
           sc[p][tt][t] = f4{c0, c0, c0, c0};
         }
         if constexpr (HP == 16) {
@@ -270,45 +282,71 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
           }
         }
       }
+    }
 
-    // Online softmax.  Scores arrive as s*c - mrow.  The running max is only
-    // raised when a tile exceeds it by more than kRescaleLog2; otherwise the
-    // stale max is kept and p may reach 2^kRescaleLog2.  acc and l share the
-    // scale, so o = acc / l is unchanged.  Fresh rows adopt their first finite max.
-    h8 pf[QT][NP];  // fp16(P) as the B operand of the PV product, per key pair
+    // Masks.  Key kb + 32p + 8g + 4tt + i is visible to query qw0 + 16t + r iff
+    // it is not past it; only pair npv-1 can hold keys past some of the wave's queries.
+    if (need_causal) {
+      const int pl = npv - 1;
 #pragma unroll
-    for (int t = 0; t < QT; ++t) {
-      if (need_causal) {
-        // key kb + 32p + 8g + 4tt + i is visible iff it is <= query qw0 + 16t + r
-        const int lim = qw0 + 16 * t + r - kb - 8 * g;
+      for (int t = 0; t < QT; ++t) {
+        const int lim = qw0 + 16 * t + r - kb - 32 * pl - 8 * g;
 #pragma unroll
-        for (int p = 0; p < NP; ++p)
+        for (int p = 0; p < NP; ++p) {
+          if (p != pl) continue;
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              if (32 * p + 4 * tt + i > lim) sc[p][tt][t][i] = -INFINITY;
+              if (4 * tt + i > lim) sc[p][tt][t][i] = -INFINITY;
+        }
       }
-      if (need_bias) {
+    }
+    if (need_bias) {
 #pragma unroll
-        for (int p = 0; p < NP; ++p)
+      for (int p = 0; p < NP; ++p) {
+        if (p >= npv) break;
+#pragma unroll
+        for (int t = 0; t < QT; ++t)
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) sc[p][tt][t][i] += kbb[32 * p + 8 * g + 4 * tt + i];
       }
+    }
+
+    // Online softmax.  Scores arrive as s*c - mrow.  The running max is only
+    // raised when a tile exceeds it by more than kRescaleLog2; otherwise the
+    // stale max is kept and p may reach 2^kRescaleLog2.  acc and l share the
+    // scale, so o = acc / l is unchanged.  Fresh rows adopt their first finite max.
+    // Each lane first takes the max of its own scores of the row; the reduction
+    // over the row's four lane groups is only needed when some lane's partial
+    // max calls for a shift (a fresh row, or one above the threshold).
+    float pm[QT];
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
       float mx = sc[0][0][t][0];
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
+      for (int p = 0; p < NP; ++p) {
+        if (p >= npv) break;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[p][tt][t][i]);
-      mx = max_over_groups(mx);
-      const bool shift_row = fresh[t] ? (mx > -INFINITY) : (mx > kRescaleLog2);
-      if (__builtin_amdgcn_ballot_w64(shift_row)) {  // rare after the first tile
+      }
+      pm[t] = mx;
+    }
+    bool any_shift = false;
+#pragma unroll
+    for (int t = 0; t < QT; ++t) any_shift |= (MAYBE_FRESH && fresh[t]) || pm[t] > kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(any_shift)) {  // the first tile, and rarely after it
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+        const float mx = max_over_groups(pm[t]);
+        const bool is_fresh = MAYBE_FRESH && fresh[t];
+        const bool shift_row = is_fresh ? (mx > -INFINITY) : (mx > kRescaleLog2);
         const float shift = shift_row ? mx : 0.f;
-        if (shift_row && !fresh[t]) {
+        if (shift_row && !is_fresh) {
           const float alpha = __builtin_amdgcn_exp2f(-shift);
           lsum_acc[t] *= alpha;
 #pragma unroll
@@ -318,33 +356,37 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
           }
         }
         if (shift_row) {
-          mrow[t] = fresh[t] ? shift : mrow[t] + shift;
+          mrow[t] = is_fresh ? shift : mrow[t] + shift;
           fresh[t] = false;
         }
 #pragma unroll
-        for (int p = 0; p < NP; ++p)
+        for (int p = 0; p < NP; ++p) {
+          if (p >= npv) break;
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) sc[p][tt][t][i] -= shift;
+        }
       }
+    }
+
+    // fp16(P) as the B operand of the PV product, then O^T += V^T P^T and the row sums of P
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
+    for (int p = 0; p < NP; ++p) {
+      if (p >= npv) break;
+      h8 pf[QT];
+#pragma unroll
+      for (int t = 0; t < QT; ++t)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) pf[t][p][4 * tt + i] = (_Float16)__builtin_amdgcn_exp2f(sc[p][tt][t][i]);
-    }
-
-    // O^T += V^T P^T, and the row sums of P
+          for (int i = 0; i < 4; ++i) pf[t][4 * tt + i] = (_Float16)__builtin_amdgcn_exp2f(sc[p][tt][t][i]);
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-#pragma unroll
-      for (int t = 0; t < QT; ++t) lsum_acc[t] = mfma32(ones_row, pf[t][p], lsum_acc[t]);
+      for (int t = 0; t < QT; ++t) lsum_acc[t] = mfma32(ones_row, pf[t], lsum_acc[t]);
       if constexpr (HP == 16) {
         const h8 va = *reinterpret_cast<const h8*>(&vtb[r * SH::LDV + 32 * p + 8 * g]);
 #pragma unroll
-        for (int t = 0; t < QT; ++t) oacc[t][0][0] = mfma32(va, pf[t][p], oacc[t][0][0]);
+        for (int t = 0; t < QT; ++t) oacc[t][0][0] = mfma32(va, pf[t], oacc[t][0][0]);
       } else {
 #pragma unroll
         for (int dt = 0; dt < SH::DT; ++dt)
@@ -353,7 +395,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
             const int drow = 32 * dt + pair_row(r, tt);
             const h8 va = *reinterpret_cast<const h8*>(&vtb[drow * SH::LDV + 32 * p + 8 * g]);
 #pragma unroll
-            for (int t = 0; t < QT; ++t) oacc[t][dt][tt] = mfma32(va, pf[t][p], oacc[t][dt][tt]);
+            for (int t = 0; t < QT; ++t) oacc[t][dt][tt] = mfma32(va, pf[t], oacc[t][dt][tt]);
           }
       }
     }
@@ -375,7 +417,10 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
     const int cur = tile & 1;
     const bool more = tile + 1 < ntiles;
     if (more) fetch((tile + 1) * KTILE);
-    process(tile * KTILE, ks_lds[cur], vt_lds[cur], kbias[cur]);
+    if (tile == 0)
+      process(0, ks_lds[cur], vt_lds[cur], kbias[cur], std::true_type{});
+    else
+      process(tile * KTILE, ks_lds[cur], vt_lds[cur], kbias[cur], std::false_type{});
     if (more) stash(cur ^ 1);
     __syncthreads();
   }
@@ -409,6 +454,303 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// 32x32 variant for head_dim 32 / 64: S^T = K Q^T and O^T = V^T P^T on
+// v_mfma_f32_32x32x16_f16, whose long issue-to-result time lets the softmax
+// VALU work of the same wave run beside it (the 16x16x32 form leaves little
+// room for that, and at these head dims the softmax is the larger cost).
+//
+// 32x32x16 operand layouts (lane l, i = l % 32, h = l / 32):
+//   A (32 x 16): row i, k = 8h .. 8h+7     B (16 x 32): column i, k = 8h .. 8h+7
+//   C (32 x 32): column i, rows 8J + 4h + I in register 4J + I  (J, I = 0..3)
+// MFMA row rho of a 32-row block is fed from row kappa(rho) of the tile
+// (keys for S^T, head dims for O^T):
+//   kappa(8J + 4h + I) = 16 (J >> 1) + 8h + 4 (J & 1) + I,
+// so the lane (i, h) accumulator register e = 8s + j (s = 0, 1; j = 0..7) holds
+// tile row 16s + 8h + j.  For S^T that is the B operand of the two 16-key steps
+// of the P V product; for O^T it is 2 x 8 consecutive head dims of query i.
+// Each lane owns one query (i) and half of its keys, so a row max is a
+// lane-local max plus one permlane32 swap.
+//
+// Scores are computed raw (s = q.k, FP16 operands, FP32 accumulate) and mapped
+// to the exponent as fma(s, |c|, -m) with the query negated when the scale is
+// negative: one rounding, as in the reference's scaled dot followed by the max
+// subtraction.  Row sums of fp16(P) come from a 16x16x32 product with a 0/1
+// A operand (rows 0 and 1 pick the queries i and i + 16 out of the P fragment
+// layout), so l sums exactly the FP16 weights that multiply V.
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f16v mfma32x32(const h8& a, const h8& b, const f16v& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int kappa32(int rho) {
+  const int J = rho >> 3, hh = (rho >> 2) & 1, I = rho & 3;
+  return 16 * (J >> 1) + 8 * hh + 4 * (J & 1) + I;
+}
+
+template <int HD, int NW, int KTILE, typename IT, typename OT, bool KEYMASK>
+__global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
+  constexpr int NT = 64 * NW;
+  using SH = AttnShape<HD, KTILE, NT>;
+  constexpr int QB = 32 * NW;     // queries per workgroup, 32 per wave
+  constexpr int NB = KTILE / 32;  // 32-key blocks per tile
+  constexpr int QS = HD / 16;     // 16-wide head-dim steps of S^T
+  constexpr int DT = HD / 32;     // 32-row head-dim tiles of O^T
+  static_assert(HD == 32 || HD == 64, "head dim");
+  static_assert(KTILE % 32 == 0 && KTILE <= NT, "key tile");
+
+  __shared__ _Float16 ks_lds[2][SH::KBUF];
+  __shared__ _Float16 vt_lds[2][SH::VBUF];
+  __shared__ float kbias[2][KTILE];
+
+  const int S = a.seq;
+  const int BH = a.batch * a.heads;
+  const int nqb = (S + QB - 1) / QB;
+  // same schedule as attention_kernel: contiguous (batch, head) ranges per XCD,
+  // longest query block first
+  int bh, qblock;
+  if ((BH & 7) == 0) {
+    const int per_xcd = BH >> 3;
+    const int slot = blockIdx.x >> 3;
+    bh = (blockIdx.x & 7) * per_xcd + slot % per_xcd;
+    qblock = nqb - 1 - slot / per_xcd;
+  } else {
+    bh = blockIdx.x % BH;
+    qblock = nqb - 1 - (int)(blockIdx.x / BH);
+  }
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int q0 = qblock * QB;
+
+  const IT* __restrict__ Q = static_cast<const IT*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const IT* __restrict__ Kp = static_cast<const IT*>(a.k) + b * a.ks[0] + h * a.ks[1];
+  const IT* __restrict__ Vp = static_cast<const IT*>(a.v) + b * a.vs[0] + h * a.vs[1];
+  OT* __restrict__ O = static_cast<OT*>(a.o) + b * a.os[0] + h * a.os[1];
+  const uint8_t* kv_valid = KEYMASK ? a.key_valid + (int64_t)b * S : nullptr;
+
+  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int qi = l & 31, hf = l >> 5;
+  const int qw0 = q0 + 32 * wave;  // first query of this wave (32-aligned, as are key blocks)
+  const int q = qw0 + qi;
+  const int trow = kappa32(qi);    // tile row this lane feeds as an A-operand row
+
+  // Q fragments (B operand of S^T): query q, head dims 16 st + 8 hf .. +7; negated for a negative scale
+  const float c = fabsf(a.c);
+  const bool neg = a.c < 0.f;
+  h8 qf[QS];
+#pragma unroll
+  for (int st = 0; st < QS; ++st) {
+    h8 v = q < S ? load8_as_half(Q + (int64_t)q * a.qs[2] + 16 * st + 8 * hf) : zero_h8();
+    if (neg) v = -v;
+    qf[st] = v;
+  }
+
+  // 0/1 A operand of the row-sum product (16x16x32 layout: lane l holds row l % 16,
+  // k = 8 (l / 16) .. +7): row 0 sums the P columns of query i, row 1 of query i + 16.
+  h8 ones;
+  {
+    const int row = l & 15, grp = l >> 4;
+    const bool one = (row == 0 && (grp & 1) == 0) || (row == 1 && (grp & 1) == 1);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ones[j] = one ? (_Float16)1.0f : (_Float16)0.0f;
+  }
+
+  float mrow = 0.f;     // running max of s*c (log2 units) of this lane's query
+  bool fresh = true;    // no visible key seen yet
+  f16v oacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[dt][e] = 0.f;
+  f4 lsum = zero4();    // lanes 0..15: [0] = l of query i, [1] = l of query i + 16
+
+  const int kv_end = a.causal ? min(q0 + QB, S) : S;
+  const int ntiles = (kv_end + KTILE - 1) / KTILE;
+
+  // ---- register prefetch / LDS staging of one K/V tile (as in attention_kernel) ----
+  h8 kreg[SH::PER_THREAD], vreg[SH::V_PER_THREAD][2];
+  float breg = 0.f;
+  const uint32_t krow_bytes = (uint32_t)(a.ks[2] * (int64_t)sizeof(IT));
+  const uint32_t vrow_bytes = (uint32_t)(a.vs[2] * (int64_t)sizeof(IT));
+  auto fetch = [&](int kb) {
+    const uint32_t rows = (uint32_t)min(KTILE, S - kb);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(Kp + (int64_t)kb * a.ks[2], rows * krow_bytes);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(Vp + (int64_t)kb * a.vs[2], rows * vrow_bytes);
+#pragma unroll
+    for (int i = 0; i < SH::PER_THREAD; ++i) {
+      const int cc = threadIdx.x + i * NT;
+      const int key = cc / SH::CPK, col = (cc % SH::CPK) * 8;
+      if (cc < SH::CHUNKS) kreg[i] = buffer_load8_as_half(kr, key * krow_bytes + col * (uint32_t)sizeof(IT), Kp);
+    }
+#pragma unroll
+    for (int i = 0; i < SH::V_PER_THREAD; ++i) {
+      const int cc = threadIdx.x + i * NT;
+      const int kp = cc % (KTILE / 2), col = (cc / (KTILE / 2)) * 8;
+      if (cc < SH::VITEMS) {
+        const uint32_t off = 2 * kp * vrow_bytes + col * (uint32_t)sizeof(IT);
+        vreg[i][0] = buffer_load8_as_half(vr, off, Vp);
+        vreg[i][1] = buffer_load8_as_half(vr, off + vrow_bytes, Vp);
+      }
+    }
+    if (threadIdx.x < KTILE) {
+      const int gk = kb + threadIdx.x;
+      bool valid = gk < S;
+      if (KEYMASK && valid) valid = kv_valid[gk] != 0;
+      breg = valid ? 0.f : -INFINITY;
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < SH::PER_THREAD; ++i) {
+      const int cc = threadIdx.x + i * NT;
+      if (cc < SH::CHUNKS) {
+        const int key = cc / SH::CPK, col = (cc % SH::CPK) * 8;
+        *reinterpret_cast<h8*>(&ks_lds[buf][key * SH::LDK + col]) = kreg[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < SH::V_PER_THREAD; ++i) {
+      const int cc = threadIdx.x + i * NT;
+      if (cc < SH::VITEMS) {
+        const int kp = cc % (KTILE / 2), col = (cc / (KTILE / 2)) * 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+          h2 pair;
+          pair[0] = vreg[i][0][j];
+          pair[1] = vreg[i][1][j];
+          *reinterpret_cast<h2*>(&vt_lds[buf][(col + j) * SH::LDV + 2 * kp]) = pair;
+        }
+      }
+    }
+    if (threadIdx.x < KTILE) kbias[buf][threadIdx.x] = breg;
+  };
+
+  // ---- one key tile ----
+  auto process = [&](const int kb, const _Float16* ksb, const _Float16* vtb, const float* kbb, auto first_tag) {
+    constexpr bool MAYBE_FRESH = decltype(first_tag)::value || KEYMASK;
+    const bool need_bias = KEYMASK || kb + KTILE > S;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int kb32 = kb + 32 * nb;
+      if (a.causal && kb32 > qw0) break;  // this block and the rest of the tile are in the wave's future
+
+      // S^T (32 keys x 32 queries), raw scores
+      f16v sc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = 0.f;
+#pragma unroll
+      for (int st = 0; st < QS; ++st) {
+        const h8 ka = *reinterpret_cast<const h8*>(&ksb[(32 * nb + trow) * SH::LDK + 16 * st + 8 * hf]);
+        sc = mfma32x32(ka, qf[st], sc);
+      }
+      // register e holds key kb32 + 16 (e >> 3) + 8 hf + (e & 7)
+      if (a.causal && kb32 == qw0) {  // the block on the diagonal: keys past the query are masked
+        const int lim = qi - 8 * hf;
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (16 * (e >> 3) + (e & 7) > lim) sc[e] = -INFINITY;
+      }
+      if (need_bias) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const float* kbp = kbb + 32 * nb + 16 * s2 + 8 * hf;
+          const float4 b0 = *reinterpret_cast<const float4*>(kbp);
+          const float4 b1 = *reinterpret_cast<const float4*>(kbp + 4);
+          sc[8 * s2 + 0] += b0.x; sc[8 * s2 + 1] += b0.y; sc[8 * s2 + 2] += b0.z; sc[8 * s2 + 3] += b0.w;
+          sc[8 * s2 + 4] += b1.x; sc[8 * s2 + 5] += b1.y; sc[8 * s2 + 6] += b1.z; sc[8 * s2 + 7] += b1.w;
+        }
+      }
+
+      // online softmax with a lazily raised max (see attention_kernel); the
+      // lane-local max decides whether the row-wide one is needed at all
+      float mx = sc[0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sc[e]);
+      const float ms = mx * c;  // this lane's max of s*c
+      const bool want = (MAYBE_FRESH && fresh) || ms - mrow > kRescaleLog2;
+      if (__builtin_amdgcn_ballot_w64(want)) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ms), __float_as_uint(ms), false, false);
+        const float full = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        const bool is_fresh = MAYBE_FRESH && fresh;
+        const bool shift_row = is_fresh ? (full > -INFINITY) : (full - mrow > kRescaleLog2);
+        float alpha = 1.f;
+        if (shift_row) {
+          if (!is_fresh) alpha = __builtin_amdgcn_exp2f(mrow - full);
+          mrow = full;
+          fresh = false;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+        // the row sums of queries (l % 16) and (l % 16) + 16 live in lanes 0..15
+        const float a0 = __shfl(alpha, l & 15), a1 = __shfl(alpha, (l & 15) + 16);
+        lsum[0] *= a0;
+        lsum[1] *= a1;
+      }
+      const float negm = -mrow;
+
+      // p = 2^(s c - m) rounded to FP16: the two 16-key B fragments
+      h8 pf[2];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(fmaf(sc[e], c, negm));
+      lsum = mfma32(ones, pf[0], lsum);
+      lsum = mfma32(ones, pf[1], lsum);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const h8 va = *reinterpret_cast<const h8*>(&vtb[(32 * dt + trow) * SH::LDV + 32 * nb + 16 * s2 + 8 * hf]);
+          oacc[dt] = mfma32x32(va, pf[s2], oacc[dt]);
+        }
+    }
+  };
+
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int tile = 0; tile < ntiles; ++tile) {
+    const int cur = tile & 1;
+    const bool more = tile + 1 < ntiles;
+    if (more) fetch((tile + 1) * KTILE);
+    if (tile == 0)
+      process(0, ks_lds[cur], vt_lds[cur], kbias[cur], std::true_type{});
+    else
+      process(tile * KTILE, ks_lds[cur], vt_lds[cur], kbias[cur], std::false_type{});
+    if (more) stash(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- normalise and store: lane (i, hf) holds head dims 32 dt + 16 s + 8 hf + j in register 8 s + j ----
+  const float a0 = __shfl(lsum[0], qi & 15), a1 = __shfl(lsum[1], qi & 15);
+  const float lrow = qi < 16 ? a0 : a1;
+  const float inv = lrow > 0.f ? 1.0f / lrow : 0.f;
+  if (q < S) {
+    OT* dst = O + (int64_t)q * a.os[2];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = oacc[dt][8 * s2 + j] * inv;
+        store8(dst + 32 * dt + 16 * s2 + 8 * hf, v);
+      }
+  }
+}
+
+template <int HD, int NW, int KTILE, typename IT, typename OT>
+static hipError_t launch_attn32(const AttnArgs& a, hipStream_t s) {
+  constexpr int QB = 32 * NW;
+  const int64_t nqb = (a.seq + QB - 1) / QB;
+  const int64_t grid = nqb * a.batch * a.heads;
+  if (grid > 0x7fffffff) return hipErrorInvalidConfiguration;
+  if (a.key_valid)
+    hipLaunchKernelGGL((attention32_kernel<HD, NW, KTILE, IT, OT, true>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a);
+  else
+    hipLaunchKernelGGL((attention32_kernel<HD, NW, KTILE, IT, OT, false>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a);
+  return hipGetLastError();
+}
+
 template <int HD, int QT, int KTILE, int NW, typename IT, typename OT>
 static hipError_t launch_attn(const AttnArgs& a, hipStream_t s) {
   constexpr int QB = 16 * QT * NW;
@@ -426,6 +768,8 @@ static hipError_t launch_attn(const AttnArgs& a, hipStream_t s) {
 
 // Tile variants (queries per wave x keys per tile x waves per workgroup):
 //   1: 16 x 64 x 4     2: 32 x 64 x 4     3: 32 x 128 x 4     4: 32 x 64 x 8     5: 16 x 128 x 4
+// and, for head_dim 32 / 64 only, the 32x32 kernel (32 queries per wave):
+//   6: 32 x 64 x 4     7: 32 x 64 x 8     8: 32 x 128 x 4
 template <int HD, typename IT, typename OT>
 static hipError_t attn_variant(int variant, const AttnArgs& a, hipStream_t s) {
   switch (variant) {
@@ -447,8 +791,24 @@ static hipError_t attn_variant_256(int variant, const AttnArgs& a, hipStream_t s
   return launch_attn<256, 1, 32, 4, IT, OT>(a, s);
 }
 
+// 32x32 variants (head_dim 32 and 64): 6: 4 waves x 64-key tiles  7: 8 waves x 64  8: 4 waves x 128
+template <int HD, typename IT, typename OT>
+static hipError_t attn32_variant(int variant, const AttnArgs& a, hipStream_t s) {
+  switch (variant) {
+    case 6: return launch_attn32<HD, 4, 64, IT, OT>(a, s);
+    case 7: return launch_attn32<HD, 8, 64, IT, OT>(a, s);
+    case 8: return launch_attn32<HD, 4, 128, IT, OT>(a, s);
+    default: return (hipError_t)MPK_EUNSUPPORTED;
+  }
+}
+
 template <typename IT, typename OT>
 static hipError_t attn_dispatch(int variant, const AttnArgs& a, int hd, hipStream_t s) {
+  if (variant >= 6) {
+    if (hd == 32) return attn32_variant<32, IT, OT>(variant, a, s);
+    if (hd == 64) return attn32_variant<64, IT, OT>(variant, a, s);
+    return (hipError_t)MPK_EUNSUPPORTED;
+  }
   switch (hd) {
     case 8: return attn_variant<8, IT, OT>(variant, a, s);
     case 16: return attn_variant<16, IT, OT>(variant, a, s);
@@ -465,10 +825,14 @@ static hipError_t attn_dispatch(int variant, const AttnArgs& a, int hd, hipStrea
 using namespace mpk;
 
 // Built-in choice, from MI355X sweeps: short sequences favour 16 queries per wave
-// (more workgroups); long ones 32 queries per wave, and 8-wave workgroups at S >= 4096.
+// (more workgroups); from 512 keys on, head dims 32 and 64 run the 32x32 kernel
+// (128-key tiles, or 8-wave workgroups at S >= 4096 and for head_dim 64), other
+// head dims 32 queries per wave and 8-wave workgroups at S >= 4096.
 extern "C" int mpk_attention_auto_variant(int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim) {
   (void)batch; (void)heads;
   if (head_dim >= 128 || seq_len < 512) return 1;
+  if (head_dim == 32) return seq_len >= 4096 ? 7 : 8;
+  if (head_dim == 64) return 7;
   return seq_len >= 4096 ? 4 : 2;
 }
 
@@ -493,7 +857,7 @@ extern "C" int mpk_causal_attention(const void* q, const void* k, const void* v,
   }
   if (batch == 0 || seq_len == 0) return MPK_OK;
   if (variant == 0) variant = mpk_attention_auto_variant(batch, heads, seq_len, head_dim);
-  if (variant < 1 || variant > 5) return MPK_EUNSUPPORTED;
+  if (variant < 1 || variant > 8) return MPK_EUNSUPPORTED;
   AttnArgs a{};
   a.q = q; a.k = k; a.v = v; a.o = o;
   for (int j = 0; j < 4; ++j) {

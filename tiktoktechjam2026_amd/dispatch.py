@@ -28,6 +28,8 @@ Tile variants (see the kernel sources for the exact tiles):
   out-proj + LN            1: 64 rows/WG           2: 128 rows/WG (d <= 128)
   fused FFN + LN           1: 16 rows/wave         2: 32 rows/wave (d <= 256)
   attention                1: 16 queries/wave      2: 32 queries/wave (hd <= 64)
+                           3-5: 128-key tiles / 8-wave workgroups
+                           6-8: 32x32-MFMA kernel (hd 32 and 64)
   layer tail / LN+QKV      1: 16 rows/wave         2: 32 rows/wave
 """
 
