@@ -104,7 +104,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
   OT* __restrict__ O = static_cast<OT*>(a.o) + b * a.os[0] + h * a.os[1];
   const uint8_t* kv_valid = KEYMASK ? a.key_valid + (int64_t)b * S : nullptr;
 
-  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63, wave = wave_id();
   const int r = l & 15, g = l >> 4;
   const int qw0 = q0 + wave * 16 * QT;       // first query of this wave
   const int qw_last = qw0 + 16 * QT - 1;     // last query of this wave
@@ -475,7 +475,12 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 // Scores are computed raw (s = q.k, FP16 operands, FP32 accumulate) and mapped
 // to the exponent as fma(s, |c|, -m) with the query negated when the scale is
 // negative: one rounding, as in the reference's scaled dot followed by the max
-// subtraction.  Row sums of fp16(P) come from a 16x16x32 product with a 0/1
+// subtraction.  (Folding c into a hi + lo split of q, as attention_kernel does,
+// doubles the S^T MFMAs; measured on MI355X that lengthens each wave's
+// MFMA -> softmax -> MFMA chain by more than the FMA it saves.)  Per score the
+// VALU runs the FMA, the exponential (half the FMA rate on gfx950, not
+// overlapped with other VALU work), the max and the FP16 conversion, which makes
+// it the binding unit at these head dims.  Row sums of fp16(P) come from a 16x16x32 product with a 0/1
 // A operand (rows 0 and 1 pick the queries i and i + 16 out of the P fragment
 // layout), so l sums exactly the FP16 weights that multiply V.
 typedef float f16v __attribute__((ext_vector_type(16)));
@@ -528,13 +533,14 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
   OT* __restrict__ O = static_cast<OT*>(a.o) + b * a.os[0] + h * a.os[1];
   const uint8_t* kv_valid = KEYMASK ? a.key_valid + (int64_t)b * S : nullptr;
 
-  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63, wave = wave_id();
   const int qi = l & 31, hf = l >> 5;
   const int qw0 = q0 + 32 * wave;  // first query of this wave (32-aligned, as are key blocks)
   const int q = qw0 + qi;
   const int trow = kappa32(qi);    // tile row this lane feeds as an A-operand row
 
-  // Q fragments (B operand of S^T): query q, head dims 16 st + 8 hf .. +7; negated for a negative scale
+  // Q fragments (B operand of S^T): query q, head dims 16 st + 8 hf .. +7; negated for a
+  // negative scale, so scores map to the exponent as fma(s, |c|, -m)
   const float c = fabsf(a.c);
   const bool neg = a.c < 0.f;
   h8 qf[QS];
@@ -627,72 +633,98 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
   };
 
   // ---- one key tile ----
-  auto process = [&](const int kb, const _Float16* ksb, const _Float16* vtb, const float* kbb, auto first_tag) {
+  // The S^T products of all of the tile's 32-key blocks are issued first; the
+  // softmax and P V of block nb then run on the VALU while the MFMAs of the
+  // later blocks are still in flight, so one wave keeps both units busy.  The
+  // running max is checked once per tile.
+  // EDGE: the tile may hold blocks in the wave's future, the diagonal block, keys
+  // past the sequence end or masked keys; steady-state tiles skip those checks.
+  auto process = [&](const int kb, const _Float16* ksb, const _Float16* vtb, const float* kbb, auto first_tag,
+                     auto edge_tag) {
     constexpr bool MAYBE_FRESH = decltype(first_tag)::value || KEYMASK;
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    // blocks [0, nbv) hold keys visible to some query of the wave (wave-uniform)
+    const int nbv = (EDGE && a.causal) ? min(NB, (qw0 - kb) / 32 + 1) : NB;
+    if (EDGE && nbv <= 0) return;
     const bool need_bias = KEYMASK || kb + KTILE > S;
+
+    // S^T (32 keys x 32 queries) per block, raw scores
+    f16v sc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      const int kb32 = kb + 32 * nb;
-      if (a.causal && kb32 > qw0) break;  // this block and the rest of the tile are in the wave's future
-
-      // S^T (32 keys x 32 queries), raw scores
-      f16v sc;
+      if (EDGE && nb >= nbv) break;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sc[e] = 0.f;
+      for (int e = 0; e < 16; ++e) sc[nb][e] = 0.f;
 #pragma unroll
       for (int st = 0; st < QS; ++st) {
         const h8 ka = *reinterpret_cast<const h8*>(&ksb[(32 * nb + trow) * SH::LDK + 16 * st + 8 * hf]);
-        sc = mfma32x32(ka, qf[st], sc);
+        sc[nb] = mfma32x32(ka, qf[st], sc[nb]);
       }
-      // register e holds key kb32 + 16 (e >> 3) + 8 hf + (e & 7)
-      if (a.causal && kb32 == qw0) {  // the block on the diagonal: keys past the query are masked
-        const int lim = qi - 8 * hf;
+    }
+    if constexpr (EDGE) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if (16 * (e >> 3) + (e & 7) > lim) sc[e] = -INFINITY;
-      }
-      if (need_bias) {
+      for (int nb = 0; nb < NB; ++nb) {
+        if (nb >= nbv) break;
+        // register e holds key kb + 32 nb + 16 (e >> 3) + 8 hf + (e & 7)
+        if (a.causal && kb + 32 * nb == qw0) {  // the block on the diagonal: keys past the query are masked
+          const int lim = qi - 8 * hf;
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const float* kbp = kbb + 32 * nb + 16 * s2 + 8 * hf;
-          const float4 b0 = *reinterpret_cast<const float4*>(kbp);
-          const float4 b1 = *reinterpret_cast<const float4*>(kbp + 4);
-          sc[8 * s2 + 0] += b0.x; sc[8 * s2 + 1] += b0.y; sc[8 * s2 + 2] += b0.z; sc[8 * s2 + 3] += b0.w;
-          sc[8 * s2 + 4] += b1.x; sc[8 * s2 + 5] += b1.y; sc[8 * s2 + 6] += b1.z; sc[8 * s2 + 7] += b1.w;
+          for (int e = 0; e < 16; ++e)
+            if (16 * (e >> 3) + (e & 7) > lim) sc[nb][e] = -INFINITY;
+        }
+        if (need_bias) {
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            const float* kbp = kbb + 32 * nb + 16 * s2 + 8 * hf;
+            const float4 b0 = *reinterpret_cast<const float4*>(kbp);
+            const float4 b1 = *reinterpret_cast<const float4*>(kbp + 4);
+            sc[nb][8 * s2 + 0] += b0.x; sc[nb][8 * s2 + 1] += b0.y;
+            sc[nb][8 * s2 + 2] += b0.z; sc[nb][8 * s2 + 3] += b0.w;
+            sc[nb][8 * s2 + 4] += b1.x; sc[nb][8 * s2 + 5] += b1.y;
+            sc[nb][8 * s2 + 6] += b1.z; sc[nb][8 * s2 + 7] += b1.w;
+          }
         }
       }
+    }
 
-      // online softmax with a lazily raised max (see attention_kernel); the
-      // lane-local max decides whether the row-wide one is needed at all
-      float mx = sc[0];
+    // online softmax with a lazily raised max (see attention_kernel); the
+    // lane-local max over the tile decides whether the row-wide one is needed at all
+    float mx = sc[0][0];
 #pragma unroll
-      for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sc[e]);
-      const float ms = mx * c;  // this lane's max of s*c
-      const bool want = (MAYBE_FRESH && fresh) || ms - mrow > kRescaleLog2;
-      if (__builtin_amdgcn_ballot_w64(want)) {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ms), __float_as_uint(ms), false, false);
-        const float full = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        const bool is_fresh = MAYBE_FRESH && fresh;
-        const bool shift_row = is_fresh ? (full > -INFINITY) : (full - mrow > kRescaleLog2);
-        float alpha = 1.f;
-        if (shift_row) {
-          if (!is_fresh) alpha = __builtin_amdgcn_exp2f(mrow - full);
-          mrow = full;
-          fresh = false;
-        }
+    for (int nb = 0; nb < NB; ++nb) {
+      if (EDGE && nb >= nbv) break;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
-        // the row sums of queries (l % 16) and (l % 16) + 16 live in lanes 0..15
-        const float a0 = __shfl(alpha, l & 15), a1 = __shfl(alpha, (l & 15) + 16);
-        lsum[0] *= a0;
-        lsum[1] *= a1;
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[nb][e]);
+    }
+    const float ms = mx * c;  // this lane's max of s*c
+    const bool want = (MAYBE_FRESH && fresh) || ms - mrow > kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(want)) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ms), __float_as_uint(ms), false, false);
+      const float full = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      const bool is_fresh = MAYBE_FRESH && fresh;
+      const bool shift_row = is_fresh ? (full > -INFINITY) : (full - mrow > kRescaleLog2);
+      float alpha = 1.f;
+      if (shift_row) {
+        if (!is_fresh) alpha = __builtin_amdgcn_exp2f(mrow - full);
+        mrow = full;
+        fresh = false;
       }
-      const float negm = -mrow;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+      // the row sums of queries (l % 16) and (l % 16) + 16 live in lanes 0..15
+      const float a0 = __shfl(alpha, l & 15), a1 = __shfl(alpha, (l & 15) + 16);
+      lsum[0] *= a0;
+      lsum[1] *= a1;
+    }
+    const float negm = -mrow;
 
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      if (EDGE && nb >= nbv) break;
       // p = 2^(s c - m) rounded to FP16: the two 16-key B fragments
       h8 pf[2];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(fmaf(sc[e], c, negm));
+      for (int e = 0; e < 16; ++e) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(fmaf(sc[nb][e], c, negm));
       lsum = mfma32(ones, pf[0], lsum);
       lsum = mfma32(ones, pf[1], lsum);
 #pragma unroll
@@ -705,20 +737,29 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
     }
   };
 
+  // One step per key tile: prefetch the next tile into registers, process this
+  // one, stage the next into the other LDS buffer, one barrier.  Tiles below the
+  // workgroup's first query (and inside the sequence) are visible to every query
+  // of every wave and run the check-free steady-state body in a loop of their
+  // own; the split point is workgroup-uniform, so every wave meets the same
+  // barriers.
+  auto step = [&](int tile, auto first_tag, auto edge_tag) {
+    const int cur = tile & 1;
+    const int kb = tile * KTILE;
+    const bool more = tile + 1 < ntiles;
+    if (more) fetch(kb + KTILE);
+    process(kb, ks_lds[cur], vt_lds[cur], kbias[cur], first_tag, edge_tag);
+    if (more) stash(cur ^ 1);
+    __syncthreads();
+  };
+  const int steady_end = KEYMASK ? 1 : max(1, min(ntiles, (a.causal ? min(q0, S) : S) / KTILE));
+
   fetch(0);
   stash(0);
   __syncthreads();
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int cur = tile & 1;
-    const bool more = tile + 1 < ntiles;
-    if (more) fetch((tile + 1) * KTILE);
-    if (tile == 0)
-      process(0, ks_lds[cur], vt_lds[cur], kbias[cur], std::true_type{});
-    else
-      process(tile * KTILE, ks_lds[cur], vt_lds[cur], kbias[cur], std::false_type{});
-    if (more) stash(cur ^ 1);
-    __syncthreads();
-  }
+  step(0, std::true_type{}, std::true_type{});
+  for (int tile = 1; tile < steady_end; ++tile) step(tile, std::false_type{}, std::false_type{});
+  for (int tile = steady_end; tile < ntiles; ++tile) step(tile, std::false_type{}, std::true_type{});
 
   // ---- normalise and store: lane (i, hf) holds head dims 32 dt + 16 s + 8 hf + j in register 8 s + j ----
   const float a0 = __shfl(lsum[0], qi & 15), a1 = __shfl(lsum[1], qi & 15);
@@ -826,13 +867,13 @@ using namespace mpk;
 
 // Built-in choice, from MI355X sweeps: short sequences favour 16 queries per wave
 // (more workgroups); from 512 keys on, head dims 32 and 64 run the 32x32 kernel
-// (128-key tiles, or 8-wave workgroups at S >= 4096 and for head_dim 64), other
-// head dims 32 queries per wave and 8-wave workgroups at S >= 4096.
+// (4-wave workgroups with 64-key tiles, 8-wave workgroups for head_dim 32 at
+// S >= 4096), other head dims 32 queries per wave and 8-wave workgroups at S >= 4096.
 extern "C" int mpk_attention_auto_variant(int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim) {
   (void)batch; (void)heads;
   if (head_dim >= 128 || seq_len < 512) return 1;
-  if (head_dim == 32) return seq_len >= 4096 ? 7 : 8;
-  if (head_dim == 64) return 7;
+  if (head_dim == 32) return seq_len >= 4096 ? 7 : 6;
+  if (head_dim == 64) return 6;
   return seq_len >= 4096 ? 4 : 2;
 }
 

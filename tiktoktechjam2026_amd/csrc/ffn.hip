@@ -56,7 +56,7 @@ __global__ __launch_bounds__(kBlock) void ffn_ln_kernel(FfnArgs a) {
   const int nchunks = (F + FC - 1) / FC;
   const int64_t ntiles = (M + BM - 1) / BM;
 
-  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63, wave = wave_id();
   const int r = l & 15, g = l >> 4;
 
   auto load_chunk = [&](int fc) {

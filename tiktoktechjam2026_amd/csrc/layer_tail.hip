@@ -155,7 +155,7 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
 
   extern __shared__ __align__(16) _Float16 lds[];
 
-  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63, wave = wave_id();
   const int r = l & 15, g = l >> 4;
 
   if constexpr (STAGE1) {

@@ -66,7 +66,7 @@ __global__ __launch_bounds__(kBlock) void linear_kernel(LinearArgs a) {
   const int64_t m0 = (int64_t)(tile / nbn) * BM;
   const int n0 = (tile % nbn) * BN;
 
-  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63, wave = wave_id();
   const int r = l & 15, g = l >> 4;
   const int wm = wave % WAVES_M, wn = wave / WAVES_M;
 
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(2 * BN) void linear_big_kernel(LinearArgs a) {
   }
   if (tile >= last) return;                     // uniform per workgroup, before any barrier
 
-  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63, wave = wave_id();
   const int r = l & 15, g = l >> 4;
   const int wm = wave & 1, wn = wave >> 1;
 

@@ -50,6 +50,11 @@ __device__ __forceinline__ f4 mfma16(const h4& a, const h4& b, const f4& c) {
 
 __device__ __forceinline__ int pair_row(int q, int t) { return 8 * (q >> 2) + 4 * t + (q & 3); }
 
+// Index of the calling wave in its workgroup, as a wave-uniform (scalar) value:
+// branches on quantities derived from it compile to scalar branches instead of
+// exec-mask divergence, and its address arithmetic stays on the scalar unit.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 __device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
 
 // ---- global loads of 8 consecutive elements as FP16 (round-to-nearest-even) ----
