@@ -76,7 +76,20 @@ struct TailShape {
   static constexpr int WQKV = WOUT + (STAGE1 ? D * LDF : 0);
   static constexpr int NBUF = WQKV + (QKV && QMODE == kQkvLds ? 3 * D * LDD : 0);
   static constexpr int TOTAL = NBUF + (QKV && QMODE == kQkvReg ? 16 * TM * kTailWaves * LDD : 0);
-  static constexpr int BYTES = TOTAL * 2;
+  // Small per-feature parameters, staged once per workgroup as FP32 after the
+  // FP16 region (offsets in floats): b_o, LN2 gamma/beta, b_in, b_out (STAGE1),
+  // the next LayerNorm's gamma/beta, and b_qkv (QKV).
+  static constexpr int P_BO = 0;
+  static constexpr int P_G2 = P_BO + (STAGE1 ? D : 0);
+  static constexpr int P_BE2 = P_G2 + (STAGE1 ? D : 0);
+  static constexpr int P_BIN = P_BE2 + (STAGE1 ? D : 0);
+  static constexpr int P_BOUT = P_BIN + (STAGE1 ? F : 0);
+  static constexpr int P_G1 = P_BOUT + (STAGE1 ? D : 0);
+  static constexpr int P_BE1 = P_G1 + D;
+  static constexpr int P_BQKV = P_BE1 + D;
+  static constexpr int NPARAM = P_BQKV + (QKV ? 3 * D : 0);
+  static constexpr int PARAM_OFF = (TOTAL + 7) / 8 * 8;  // halves; 16-byte aligned
+  static constexpr int BYTES = PARAM_OFF * 2 + NPARAM * 4;
 };
 
 // Copy a [rows, cols] FP16 matrix (row-major, cols % 8 == 0) into LDS with row stride ld.
@@ -86,6 +99,21 @@ __device__ __forceinline__ void stage_matrix(_Float16* dst, const _Float16* src,
     const int row = c / cpr, col = (c % cpr) * 8;
     *reinterpret_cast<h8*>(&dst[row * ld + col]) = *reinterpret_cast<const h8*>(&src[(int64_t)row * cols + col]);
   }
+}
+
+// Copy n FP16 (as_half) or FP32 parameters into the FP32 LDS parameter block.
+__device__ __forceinline__ void stage_params(float* dst, const _Float16* src, int n) {
+  for (int i = threadIdx.x; i < n; i += kTailThreads) dst[i] = (float)src[i];
+}
+__device__ __forceinline__ void stage_params(float* dst, const float* src, int n) {
+  for (int i = threadIdx.x; i < n; i += kTailThreads) dst[i] = src[i];
+}
+
+// 8 consecutive FP32 parameters from LDS.
+__device__ __forceinline__ void lds8(const float* p, float* v) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
 // Row statistics of v (lane holds one row, features 32p + 8g + j; the row is spread over the 4 lane groups).
@@ -118,22 +146,28 @@ struct TileIn {
 template <int D, int TM, bool STAGE1>
 __device__ __forceinline__ void load_tile(TileIn<D, TM, STAGE1>& in, const TailArgs& a, int64_t m0, int r, int g) {
   constexpr int PN = D / 32;
+  typedef float v4 __attribute__((ext_vector_type(4)));
+  // buffer resources over the rows that exist: rows past M read as zeros
+  const uint32_t rows = (uint32_t)(a.m - m0 <= 0 ? 0 : (a.m - m0 < 16 * TM ? a.m - m0 : 16 * TM));
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + m0 * D, rows * (uint32_t)(D * 4));
 #pragma unroll
   for (int t = 0; t < TM; ++t) {
-    const int64_t m = m0 + 16 * t + r;
-    const bool valid = m < a.m;
+    const uint32_t row = (uint32_t)(16 * t + r);
     if constexpr (STAGE1) {
+      const __amdgpu_buffer_rsrc_t crs = make_rsrc(a.ctx + m0 * D, rows * (uint32_t)(D * 2));
 #pragma unroll
       for (int ks = 0; ks < PN; ++ks)
-        in.ctx[t][ks] = valid ? *reinterpret_cast<const h8*>(a.ctx + m * D + ks * 32 + 8 * g) : zero_h8();
+        in.ctx[t][ks] = buffer_load8_as_half(crs, (row * D + ks * 32 + 8 * g) * 2u, a.ctx);
     }
 #pragma unroll
     for (int p = 0; p < PN; ++p) {
-      if (valid) {
-        load8_f32(a.x + m * D + 32 * p + 8 * g, in.x[t][p]);
-      } else {
+      const uint32_t off = (row * D + 32 * p + 8 * g) * 4u;
+      const v4 lo = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+      const v4 hi = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off + 16, 0, 0));
 #pragma unroll
-        for (int j = 0; j < 8; ++j) in.x[t][p][j] = 0.f;
+      for (int j = 0; j < 4; ++j) {
+        in.x[t][p][j] = lo[j];
+        in.x[t][p][4 + j] = hi[j];
       }
     }
   }
@@ -164,6 +198,20 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
     stage_matrix(lds + SH::WOUT, a.wout, D, F, SH::LDF);
   }
   if constexpr (QKV && QMODE == kQkvLds) stage_matrix(lds + SH::WQKV, a.wqkv, 3 * D, D, SH::LDD);
+  // Biases, gammas and betas live in LDS for the whole kernel: read inside the
+  // per-tile dependency chain, global loads would put a memory latency between
+  // every product and its epilogue.
+  float* prm = reinterpret_cast<float*>(lds + SH::PARAM_OFF);
+  if constexpr (STAGE1) {
+    stage_params(prm + SH::P_BO, a.bo, D);
+    stage_params(prm + SH::P_G2, a.g2, D);
+    stage_params(prm + SH::P_BE2, a.be2, D);
+    stage_params(prm + SH::P_BIN, a.bin, F);
+    stage_params(prm + SH::P_BOUT, a.bout, D);
+  }
+  stage_params(prm + SH::P_G1, a.g1, D);
+  stage_params(prm + SH::P_BE1, a.be1, D);
+  if constexpr (QKV) stage_params(prm + SH::P_BQKV, a.bqkv, 3 * D);
   h8 wq[QKV && QMODE == kQkvReg ? QNT : 1][KS];
   if constexpr (QKV && QMODE == kQkvReg) {
 #pragma unroll
@@ -185,6 +233,9 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
   for (; tile < ntiles; tile += gridDim.x) {
     const int64_t wg0 = tile * ROWS;
     const int64_t m0 = wg0 + wave * 16 * TM;
+    // rows of this wave / workgroup that exist (stores to the others are dropped by the buffer resource)
+    const uint32_t wrows = (uint32_t)(M - m0 <= 0 ? 0 : (M - m0 < 16 * TM ? M - m0 : 16 * TM));
+    const uint32_t grows = (uint32_t)(M - wg0 < ROWS ? M - wg0 : ROWS);
     TileIn<D, TM, STAGE1> nxt;
     if (tile + gridDim.x < ntiles) load_tile<D, TM, STAGE1>(nxt, a, (tile + gridDim.x) * ROWS + wave * 16 * TM, r, g);
 
@@ -213,7 +264,7 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
 #pragma unroll
         for (int p = 0; p < PN; ++p) {
           float bv[8];
-          load8_f16_to_f32(a.bo + 32 * p + 8 * g, bv);
+          lds8(prm + SH::P_BO + 32 * p + 8 * g, bv);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             xr[t][p][i] = (acc[p][0][i] + bv[i]) + cur.x[t][p][i];
@@ -226,8 +277,8 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
         for (int p = 0; p < PN; ++p) {
           const int n = 32 * p + 8 * g;
           float gm[8], bt[8];
-          load8_f32(a.g2 + n, gm);
-          load8_f32(a.be2 + n, bt);
+          lds8(prm + SH::P_G2 + n, gm);
+          lds8(prm + SH::P_BE2 + n, bt);
 #pragma unroll
           for (int j = 0; j < 8; ++j) n2f[t][p][j] = (_Float16)((xr[t][p][j] - mean) * rstd * gm[j] + bt[j]);
         }
@@ -239,7 +290,7 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
       for (int t = 0; t < TM; ++t)
 #pragma unroll
         for (int p = 0; p < PN; ++p) yacc[t][p][0] = yacc[t][p][1] = zero4();
-#pragma unroll 1
+#pragma unroll 2
       for (int fq = 0; fq < FQ; ++fq) {
         f4 hacc[TM][2];
 #pragma unroll
@@ -254,7 +305,7 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
             for (int t = 0; t < TM; ++t) hacc[t][tt] = mfma32(w, n2f[t][ks], hacc[t][tt]);
           }
         float bi[8];
-        load8_f16_to_f32(a.bin + 32 * fq + 8 * g, bi);
+        lds8(prm + SH::P_BIN + 32 * fq + 8 * g, bi);
         h8 hb[TM];
 #pragma unroll
         for (int t = 0; t < TM; ++t)
@@ -274,20 +325,20 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
           }
         __builtin_amdgcn_sched_barrier(0);
       }
+      const __amdgpu_buffer_rsrc_t xres = make_rsrc(a.x_out + m0 * D, wrows * (uint32_t)(D * 4));
 #pragma unroll
       for (int t = 0; t < TM; ++t) {
-        const int64_t m = m0 + 16 * t + r;
 #pragma unroll
         for (int p = 0; p < PN; ++p) {
           const int n = 32 * p + 8 * g;
           float bv[8];
-          load8_f16_to_f32(a.bout + n, bv);
+          lds8(prm + SH::P_BOUT + n, bv);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             xr[t][p][i] = (yacc[t][p][0][i] + bv[i]) + xr[t][p][i];
             xr[t][p][4 + i] = (yacc[t][p][1][i] + bv[4 + i]) + xr[t][p][4 + i];
           }
-          if (m < M) store8(a.x_out + m * D + n, xr[t][p]);
+          buffer_store8(xres, (uint32_t)((16 * t + r) * D + n) * 4u, xr[t][p], a.x_out);
         }
       }
     } else {
@@ -301,21 +352,22 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
 
     // ---- next LayerNorm, then the next layer's QKV projection (or the final output) ----
     h8 n1f[TM][KS];
+    const __amdgpu_buffer_rsrc_t ores = make_rsrc(static_cast<float*>(a.out) + (LAST ? m0 * D : 0),
+                                                  LAST ? wrows * (uint32_t)(D * 4) : 0u);
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
-      const int64_t m = m0 + 16 * t + r;
       float mean, rstd;
       row_stats<PN>(xr[t], inv_d, a.eps1, mean, rstd);
 #pragma unroll
       for (int p = 0; p < PN; ++p) {
         const int n = 32 * p + 8 * g;
         float gm[8], bt[8], o[8];
-        load8_f32(a.g1 + n, gm);
-        load8_f32(a.be1 + n, bt);
+        lds8(prm + SH::P_G1 + n, gm);
+        lds8(prm + SH::P_BE1 + n, bt);
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = (xr[t][p][j] - mean) * rstd * gm[j] + bt[j];
         if constexpr (LAST) {
-          if (m < M) store8(static_cast<float*>(a.out) + m * D + n, o);
+          buffer_store8(ores, (uint32_t)((16 * t + r) * D + n) * 4u, o, static_cast<float*>(a.out));
         } else {
 #pragma unroll
           for (int j = 0; j < 8; ++j) n1f[t][p][j] = (_Float16)o[j];
@@ -325,6 +377,7 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
 
     if constexpr (QKV && QMODE == kQkvLds) {
       _Float16* qkv = static_cast<_Float16*>(a.out);
+      const __amdgpu_buffer_rsrc_t qres = make_rsrc(qkv + m0 * (3 * D), wrows * (uint32_t)(3 * D * 2));
 #pragma unroll 1
       for (int op = 0; op < QP; ++op) {
         f4 qacc[TM][2];
@@ -341,17 +394,16 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
           }
         const int n = 32 * op + 8 * g;
         float bv[8];
-        load8_f16_to_f32(a.bqkv + n, bv);
+        lds8(prm + SH::P_BQKV + n, bv);
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
-          const int64_t m = m0 + 16 * t + r;
           float v[8];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             v[i] = qacc[t][0][i] + bv[i];
             v[4 + i] = qacc[t][1][i] + bv[4 + i];
           }
-          if (m < M) store8(qkv + m * (3 * D) + n, v);
+          buffer_store8(qres, (uint32_t)((16 * t + r) * (3 * D) + n) * 2u, v, qkv);
         }
       }
     }
@@ -371,25 +423,28 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
 #pragma unroll
       for (int nt = 0; nt < QNT; ++nt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) bq[nt][i] = (float)a.bqkv[ncol0 + 16 * nt + 4 * g + i];
+        for (int i = 0; i < 4; ++i) bq[nt][i] = prm[SH::P_BQKV + ncol0 + 16 * nt + 4 * g + i];
+      const __amdgpu_buffer_rsrc_t qres = make_rsrc(qkv + wg0 * (3 * D), grows * (uint32_t)(3 * D * 2));
 #pragma unroll 2
       for (int mt = 0; mt < ROWS / 16; ++mt) {
         h8 bn[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
           bn[ks] = *reinterpret_cast<const h8*>(&nbuf[(16 * mt + r) * SH::LDD + ks * 32 + 8 * g]);
-        const int64_t m = wg0 + 16 * mt + r;
+        // the QNT column tiles are independent MFMA chains: interleave them
+        f4 acc[QNT];
+#pragma unroll
+        for (int nt = 0; nt < QNT; ++nt) acc[nt] = zero4();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int nt = 0; nt < QNT; ++nt) acc[nt] = mfma32(wq[nt][ks], bn[ks], acc[nt]);
 #pragma unroll
         for (int nt = 0; nt < QNT; ++nt) {
-          f4 acc = zero4();
+          float o[4];
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) acc = mfma32(wq[nt][ks], bn[ks], acc);
-          if (m < M) {
-            h4 o;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = (_Float16)(acc[i] + bq[nt][i]);
-            *reinterpret_cast<h4*>(qkv + m * (3 * D) + ncol0 + 16 * nt + 4 * g) = o;
-          }
+          for (int i = 0; i < 4; ++i) o[i] = acc[nt][i] + bq[nt][i];
+          buffer_store4(qres, (uint32_t)((16 * mt + r) * (3 * D) + ncol0 + 16 * nt + 4 * g) * 2u, o);
         }
       }
       __syncthreads();  // nbuf is rewritten by the next tile

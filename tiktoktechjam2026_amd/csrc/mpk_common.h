@@ -96,6 +96,35 @@ __device__ __forceinline__ h8 buffer_load8_as_half(__amdgpu_buffer_rsrc_t r, uin
   return h;
 }
 
+// Bounds-checked stores through the same kind of buffer resource: a store whose
+// 16-byte (8-byte) chunk starts at or past the resource's size is dropped by the
+// hardware, so row tiles that run past the last row need no per-lane branch.
+__device__ __forceinline__ void buffer_store8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, const float* v,
+                                              _Float16*) {
+  h8 h;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) h[j] = (_Float16)v[j];
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, h), r, byte_off, 0, 0);
+}
+
+__device__ __forceinline__ void buffer_store8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, const float* v, float*) {
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  typedef float v4 __attribute__((ext_vector_type(4)));
+  const v4 a = {v[0], v[1], v[2], v[3]};
+  const v4 b = {v[4], v[5], v[6], v[7]};
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), r, byte_off, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, b), r, byte_off + 16, 0, 0);
+}
+
+__device__ __forceinline__ void buffer_store4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, const float* v) {
+  h4 h;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) h[j] = (_Float16)v[j];
+  typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, h), r, byte_off, 0, 0);
+}
+
 __device__ __forceinline__ h8 zero_h8() {
   h8 r;
 #pragma unroll
