@@ -86,6 +86,24 @@ int mpk_linear_residual_layernorm(const void* x, int x_dtype, const void* w, con
 int mpk_linear_residual_layernorm_auto_variant(int64_t m, int32_t d);
 
 /*
+ * Projection with a different input width + residual + LayerNorm, on 256 x 256
+ * GEMM tiles whose LayerNorm statistics are exchanged across waves in LDS:
+ *   residual_out = fp16(x) * w^T + b + residual            (FP32)
+ *   normalized_out = LayerNorm(residual_out) * gamma + beta
+ * x: [m, k] in x_dtype; w: [n, k] FP16; b: [n] FP16; residual, residual_out:
+ * [m, n] FP32 (residual_out may alias residual); gamma, beta: [n] FP32.
+ * n == 256, k % 8 == 0.
+ * Replaces, for the wide route, the reference's FFN-output projection plus its
+ * residual add and the next LayerNorm (generic FFN mixed_precision/transformer.py:664-672
+ * followed by mixed_add_layer_norm / fused_add_layer_norm at :674-690); with k == n it
+ * is mixed_linear_add_layer_norm (mixed_precision/triton_linear.py:272-324).
+ */
+int mpk_linear_add_layernorm(const void* x, int x_dtype, const void* w, const void* b,
+                             const float* residual, const float* gamma, const float* beta,
+                             float* residual_out, void* normalized_out, int normalized_dtype,
+                             int64_t m, int32_t n, int32_t k, float eps, void* stream);
+
+/*
  * Whole FFN + residual + LayerNorm, hidden activation kept on chip:
  *   h = GELU_erf(fp16(x) * w_in^T + b_in)                 (FP32, then FP16)
  *   residual_out = h * w_out^T + b_out + residual          (FP32)

@@ -177,9 +177,8 @@ def test_mixed_linear_3d_input(hip_device):
     _close(y.reshape(-1, 384), _ref_linear(x.reshape(-1, 128), lin, False), 2 ** -10, 2 ** -10, "3d")
 
 
-@pytest.mark.parametrize("d", [32, 64, 128, 256, 512])
+@pytest.mark.parametrize("d,variant", [(d, v) for d in (32, 64, 128, 256, 512) for v in (1, 2)] + [(256, 3)])
 @pytest.mark.parametrize("m", [7, 1000, 8192])
-@pytest.mark.parametrize("variant", [1, 2])
 def test_linear_residual_layernorm(hip_device, d, m, variant):
     from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear_add_layer_norm
 
@@ -197,6 +196,60 @@ def test_linear_residual_layernorm(hip_device, d, m, variant):
             _close(r_out, r64, 2e-5 * math.sqrt(d), 1e-6, "residual_out")
             tol = 5e-5 if out_dtype == torch.float32 else 2 ** -10
             _close(n_out, _ln64(r64, norm), tol, tol, "normalized_out")
+
+
+@pytest.mark.parametrize("k", [256, 1024, 136])
+@pytest.mark.parametrize("m", [7, 300, 5000])
+def test_linear_residual_layer_norm_wide(hip_device, k, m):
+    """256 x 256 GEMM tiles with the cross-wave LayerNorm epilogue (n = 256, any k % 8 == 0):
+    ragged rows (m not a multiple of the 256-row tile), K not a multiple of the 64-wide chunk,
+    FP16/FP32 inputs and outputs, and the in-place form (residual_out aliasing residual)."""
+    from tiktoktechjam2026_amd import _lib
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear_residual_layer_norm
+
+    n = 256
+    lin = _linear(k, n, hip_device, 25)
+    norm = _norm(n, hip_device, 26)
+    x = _randn((m, k), 27)
+    resid = _randn((m, n), 28, 2.0)
+    r64 = _ref_linear(x, lin, False) + resid.double()
+    for in_dtype in (torch.float16, torch.float32):
+        for out_dtype in (torch.float16, torch.float32):
+            r_out, n_out = mixed_linear_residual_layer_norm(
+                x.to(hip_device, in_dtype), lin, resid.to(hip_device), norm, normalized_dtype=out_dtype,
+            )
+            _close(r_out, r64, 2e-5 * math.sqrt(k), 1e-6, "wide residual_out")
+            tol = 5e-5 if out_dtype == torch.float32 else 2 ** -10
+            _close(n_out, _ln64(r64, norm), tol, tol, "wide normalized_out")
+    # in place: residual_out is the residual buffer
+    xr = x.to(hip_device, torch.float16)
+    rr = resid.to(hip_device).clone()
+    nn_out = torch.empty(m, n, device=hip_device, dtype=torch.float16)
+    lib = _lib.load()
+    _lib.check(
+        lib.mpk_linear_add_layernorm(
+            xr.data_ptr(), _lib.F16, lin.weight.data_ptr(), lin.bias.data_ptr(), rr.data_ptr(),
+            norm.weight.data_ptr(), norm.bias.data_ptr(), rr.data_ptr(), nn_out.data_ptr(), _lib.F16, m, n, k,
+            float(norm.eps), _lib.stream_handle(hip_device),
+        ),
+        "mpk_linear_add_layernorm",
+    )
+    _close(rr, r64, 2e-5 * math.sqrt(k), 1e-6, "in-place residual_out")
+    _close(nn_out, _ln64(r64, norm), 2 ** -10, 2 ** -10, "in-place normalized_out")
+
+
+def test_linear_residual_layer_norm_wide_rejects(hip_device):
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear_residual_layer_norm
+
+    norm = _norm(128, hip_device, 1)
+    lin = _linear(256, 128, hip_device, 2)  # out_features != 256
+    with pytest.raises(ValueError):
+        mixed_linear_residual_layer_norm(torch.zeros(4, 256, device=hip_device, dtype=torch.float16), lin,
+                                         torch.zeros(4, 128, device=hip_device), norm)
+    lin2 = _linear(256, 256, hip_device, 3)
+    with pytest.raises(ValueError):  # residual on the CPU
+        mixed_linear_residual_layer_norm(torch.zeros(4, 256, device=hip_device, dtype=torch.float16), lin2,
+                                         torch.zeros(4, 256), _norm(256, hip_device, 4))
 
 
 @pytest.mark.parametrize("d,f", [(128, 128), (32, 64), (64, 96), (256, 1024), (512, 2048), (128, 512)])

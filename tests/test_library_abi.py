@@ -61,6 +61,23 @@ def test_host_side_argument_rejection(built_library):
         lib.mpk_linear_residual_layernorm(fake, 1, fake, fake, fake, fake, fake, fake, fake, 1, 10, 96, 1e-5, 0, null)
         == _lib.MPK_EUNSUPPORTED
     )
+    # the wide LayerNorm-epilogue GEMM takes n == 256 only, k % 8 == 0
+    assert (
+        lib.mpk_linear_add_layernorm(fake, 1, fake, fake, fake, fake, fake, fake, fake, 1, 10, 128, 256, 1e-5, null)
+        == _lib.MPK_EUNSUPPORTED
+    )
+    assert (
+        lib.mpk_linear_add_layernorm(fake, 1, fake, fake, fake, fake, fake, fake, fake, 1, 10, 256, 100, 1e-5, null)
+        == _lib.MPK_EUNSUPPORTED
+    )
+    assert (
+        lib.mpk_linear_add_layernorm(fake, 1, fake, fake, null, fake, fake, fake, fake, 1, 10, 256, 256, 1e-5, null)
+        == _lib.MPK_EINVAL
+    )
+    assert (
+        lib.mpk_linear_residual_layernorm(fake, 1, fake, fake, fake, fake, fake, fake, fake, 1, 10, 128, 1e-5, 3, null)
+        == _lib.MPK_EUNSUPPORTED
+    )
     assert (
         lib.mpk_ffn_residual_layernorm(
             fake, 1, fake, fake, fake, fake, fake, fake, fake, fake, fake, 1, 10, 128, 100, 1e-5, 0, null
@@ -85,6 +102,7 @@ def test_auto_variant_queries(built_library):
     lib = built_library
     assert lib.mpk_linear_auto_variant(65536, 384, 128) in (1, 2, 3, 4)
     assert lib.mpk_linear_residual_layernorm_auto_variant(65536, 128) in (1, 2)
+    assert lib.mpk_linear_residual_layernorm_auto_variant(262144, 256) == 3
     assert lib.mpk_ffn_residual_layernorm_auto_variant(65536, 128, 128) in (1, 2)
     assert lib.mpk_attention_auto_variant(64, 4, 1024, 32) in range(1, 9)
     # the 32x32 kernel variants (6..8) only for head_dim 32 / 64

@@ -57,6 +57,13 @@ SIGNATURES = {
         ],
     ),
     "mpk_linear_residual_layernorm_auto_variant": (_c_int, [_c_i64, _c_i32]),
+    "mpk_linear_add_layernorm": (
+        _c_int,
+        [
+            _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+            _c_int, _c_i64, _c_i32, _c_i32, _c_float, _c_void_p,
+        ],
+    ),
     "mpk_ffn_residual_layernorm": (
         _c_int,
         [

@@ -24,7 +24,13 @@
 
 namespace mpk {
 
-enum Epilogue : int { kEpiBias = 0, kEpiBiasGelu = 1, kEpiResidualLN = 2, kEpiBiasResidual = 3 };
+enum Epilogue : int {
+  kEpiBias = 0,
+  kEpiBiasGelu = 1,
+  kEpiResidualLN = 2,      // whole rows per wave (row-owning kernel)
+  kEpiBiasResidual = 3,
+  kEpiResidualLNTile = 4,  // large tiles: a row spans several waves, statistics exchanged through LDS
+};
 
 struct LinearArgs {
   const void* x;
@@ -236,6 +242,7 @@ __global__ __launch_bounds__(2 * BN) void linear_big_kernel(LinearArgs a) {
   static_assert(XCH * NT == BM * CPR && WCH * NT == BN * CPR, "staging split");
   static_assert(EPI != kEpiResidualLN, "row LayerNorm needs whole rows per wave");
   static_assert(STAGES == 1 || STAGES == 2, "one or two LDS stages");
+  static_assert(EPI != kEpiResidualLNTile || STAGES == 2, "the LayerNorm epilogue uses the idle LDS stage");
 
   __shared__ _Float16 xs[STAGES][BM * LD];
   __shared__ _Float16 ws[STAGES][BN * LD];
@@ -343,6 +350,108 @@ __global__ __launch_bounds__(2 * BN) void linear_big_kernel(LinearArgs a) {
     }
   };
   OT* Y = static_cast<OT*>(a.y);  // may alias a.residual (in-place residual add)
+  // LayerNorm epilogue (N == BN: the tile holds whole rows, spread over the
+  // BN/64 waves of a row half).  R' = acc + b + R, then two-pass FP32 row
+  // statistics: each wave reduces its 64 features per row across its four lane
+  // groups, the per-wave partial sums meet in the idle LDS stage, and every
+  // wave finishes the same row sums in the same order.
+  auto epilogue_ln = [&](int etile, int obuf) {
+    constexpr int NWN = BN / WN;  // waves across a row
+    // scratch in the idle stage: [2 passes][NWN][BM] partial row sums, then gamma and beta
+    float* red = reinterpret_cast<float*>(&xs[obuf][0]);
+    float* gam = red + 2 * NWN * BM;
+    float* bet = gam + BN;
+    const int64_t m0 = (int64_t)(etile / nbn) * BM;
+    const float inv_n = 1.0f / (float)N;
+    for (int i = threadIdx.x; i < BN; i += NT) {
+      gam[i] = a.gamma[i];
+      bet[i] = a.beta[i];
+    }
+    // pass 1: R' in place of the accumulators, row sums
+    {
+      float bv[PN][8];
+#pragma unroll
+      for (int p = 0; p < PN; ++p) load8_f16_to_f32(a.bias + wn * WN + 32 * p + 8 * g, bv[p]);
+#pragma unroll
+      for (int t = 0; t < TM; ++t) {
+        const int row = wm * WM + 16 * t + r;
+        const int64_t m = m0 + row;
+        float sum = 0.f;
+#pragma unroll
+        for (int p = 0; p < PN; ++p) {
+          const int n = wn * WN + 32 * p + 8 * g;
+          float rv[8];
+          if (m < M) {
+            load8_f32(a.residual + m * N + n, rv);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) rv[j] = 0.f;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc[p][0][t][i] = (acc[p][0][t][i] + bv[p][i]) + rv[i];
+            acc[p][1][t][i] = (acc[p][1][t][i] + bv[p][4 + i]) + rv[4 + i];
+            sum += acc[p][0][t][i] + acc[p][1][t][i];
+          }
+        }
+        sum = sum_over_groups(sum);
+        if (g == 0) red[wn * BM + row] = sum;
+      }
+    }
+    __syncthreads();
+    auto row_mean = [&](int row) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < NWN; ++w) sum += red[w * BM + row];
+      return sum * inv_n;
+    };
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+      const int row = wm * WM + 16 * t + r;
+      const float mean = row_mean(row);
+      float sq = 0.f;
+#pragma unroll
+      for (int p = 0; p < PN; ++p)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float c = acc[p][tt][t][i] - mean;
+            sq += c * c;
+          }
+      sq = sum_over_groups(sq);
+      if (g == 0) red[(NWN + wn) * BM + row] = sq;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+      const int row = wm * WM + 16 * t + r;
+      const int64_t m = m0 + row;
+      const float mean = row_mean(row);
+      float sq = 0.f;
+#pragma unroll
+      for (int w = 0; w < NWN; ++w) sq += red[(NWN + w) * BM + row];
+      const float rstd = rsqrtf(sq * inv_n + a.eps);
+      if (m >= M) continue;
+#pragma unroll
+      for (int p = 0; p < PN; ++p) {
+        const int n = wn * WN + 32 * p + 8 * g;
+        float v[8], o[8], gm[8], bt[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = acc[p][0][t][i];
+          v[4 + i] = acc[p][1][t][i];
+        }
+        store8(a.residual_out + m * N + n, v);
+        load8_f32(gam + n, gm);
+        load8_f32(bet + n, bt);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = (v[j] - mean) * rstd * gm[j] + bt[j];
+        store8(static_cast<OT*>(a.y) + m * N + n, o);
+      }
+    }
+    __syncthreads();  // the scratch stage is restaged next
+  };
   auto epilogue = [&](int etile) {
     const int64_t m0 = (int64_t)(etile / nbn) * BM;
     const int n0 = (etile % nbn) * BN;
@@ -391,7 +500,10 @@ __global__ __launch_bounds__(2 * BN) void linear_big_kernel(LinearArgs a) {
     if (more) fetch(ntile, nc * BK);
     compute(buf);
     if (c == nchunks - 1) {
-      epilogue(tile);
+      if constexpr (EPI == kEpiResidualLNTile)
+        epilogue_ln(tile, buf ^ 1);
+      else
+        epilogue(tile);
 #pragma unroll
       for (int p = 0; p < PN; ++p)
 #pragma unroll
@@ -485,6 +597,12 @@ static hipError_t linear_ln_d(int variant, const LinearArgs& a, hipStream_t s) {
 
 template <typename XT, typename OT>
 static hipError_t linear_ln(int variant, const LinearArgs& a, hipStream_t s) {
+  // variant 3: 256 x 256 GEMM tiles with the cross-wave LayerNorm epilogue (N = 256, any K)
+  if (variant == 3) {
+    if (a.n != 256) return (hipError_t)MPK_EUNSUPPORTED;
+    return launch_linear_big<256, 2, XT, kEpiResidualLNTile, OT>(a, s);
+  }
+  if (a.k != a.n) return (hipError_t)MPK_EUNSUPPORTED;
   switch (a.n) {
     case 32: return linear_ln_d<32, 32, XT, OT>(variant, a, s);
     case 64: return linear_ln_d<64, 64, XT, OT>(variant, a, s);
@@ -538,7 +656,7 @@ extern "C" int mpk_linear(const void* x, int x_dtype, const void* w, const void*
 }
 
 extern "C" int mpk_linear_residual_layernorm_auto_variant(int64_t m, int32_t d) {
-  (void)d;
+  if (d == 256) return 3;
   return m >= 128 * 512 ? 2 : 1;
 }
 
@@ -556,6 +674,7 @@ extern "C" int mpk_linear_residual_layernorm(const void* x, int x_dtype, const v
     return MPK_EALIGN;
   if (m == 0) return MPK_OK;
   if (variant == 0) variant = mpk_linear_residual_layernorm_auto_variant(m, d);
+  if (variant < 1 || variant > 3) return MPK_EUNSUPPORTED;
   LinearArgs a{};
   a.x = x; a.w = static_cast<const _Float16*>(w); a.bias = static_cast<const _Float16*>(b); a.y = normalized_out;
   a.residual = residual; a.gamma = gamma; a.beta = beta; a.residual_out = residual_out;
@@ -582,5 +701,31 @@ extern "C" int mpk_linear_residual(const void* x, int x_dtype, const void* w, co
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const hipError_t e = x_dtype == kF32 ? linear_variant<float, kEpiBiasResidual, float>(variant, a, s)
                                        : linear_variant<_Float16, kEpiBiasResidual, float>(variant, a, s);
+  return (int)e;
+}
+
+extern "C" int mpk_linear_add_layernorm(const void* x, int x_dtype, const void* w, const void* b,
+                                        const float* residual, const float* gamma, const float* beta,
+                                        float* residual_out, void* normalized_out, int normalized_dtype, int64_t m,
+                                        int32_t n, int32_t k, float eps, void* stream) {
+  if (!x || !w || !b || !residual || !gamma || !beta || !residual_out || !normalized_out || m < 0 || n <= 0 ||
+      k <= 0)
+    return MPK_EINVAL;
+  if ((x_dtype != kF32 && x_dtype != kF16) || (normalized_dtype != kF32 && normalized_dtype != kF16))
+    return MPK_EINVAL;
+  if (n != 256 || k % 8 != 0) return MPK_EUNSUPPORTED;
+  if (!aligned16(x) || !aligned16(w) || !aligned16(b) || !aligned16(residual) || !aligned16(gamma) ||
+      !aligned16(beta) || !aligned16(residual_out) || !aligned16(normalized_out))
+    return MPK_EALIGN;
+  if (m == 0) return MPK_OK;
+  LinearArgs a{};
+  a.x = x; a.w = static_cast<const _Float16*>(w); a.bias = static_cast<const _Float16*>(b); a.y = normalized_out;
+  a.residual = residual; a.gamma = gamma; a.beta = beta; a.residual_out = residual_out;
+  a.m = m; a.n = n; a.k = k; a.eps = eps;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  const bool xf = x_dtype == kF32, of = normalized_dtype == kF32;
+  if (xf) e = of ? linear_ln<float, float>(3, a, s) : linear_ln<float, _Float16>(3, a, s);
+  else e = of ? linear_ln<_Float16, float>(3, a, s) : linear_ln<_Float16, _Float16>(3, a, s);
   return (int)e;
 }

@@ -18,6 +18,12 @@ the shape is only
   library's built-in table (``mpk_*_auto_variant``); entries in ``TUNED``
   override it for shapes measured on MI355X (256 CUs, 64-lane waves).
 
+At d_model 256 (``WIDE_LN_EPILOGUE_WIDTH``) the GEMM route's two residual
+projections carry the next LayerNorm in their epilogue (``wide_ln_epilogue``):
+a 256 x 256 output tile holds whole rows, so the row statistics are exchanged
+across its waves in LDS and no separate LayerNorm launch re-reads the residual
+stream.
+
 When the whole layer tail fits one kernel (``LAYER_TAIL_SHAPES``) the forward
 runs 1 + 2L launches: LayerNorm+QKV, then per layer attention and the fused
 tail (out-proj+LN2+FFN+LN1'+QKV', or the final LayerNorm on the last layer).
@@ -26,6 +32,7 @@ Tile variants (see the kernel sources for the exact tiles):
   projections              1: 128x128 (2x2 waves)  2: 128x64  3: 128x32  4: 64x128
                            5: 256x128 double-buffered  6: 256x128 single-buffered
   out-proj + LN            1: 64 rows/WG           2: 128 rows/WG (d <= 128)
+                           3: 256x256 GEMM tiles, cross-wave LayerNorm (d = 256)
   fused FFN + LN           1: 16 rows/wave         2: 32 rows/wave (d <= 256)
   attention                1: 16 queries/wave      2: 32 queries/wave (hd <= 64)
                            3-5: 128-key tiles / 8-wave workgroups
@@ -48,6 +55,8 @@ LAYER_TAIL_SHAPES = frozenset({(32, 32), (32, 64), (32, 128), (64, 64), (64, 128
 LAYERNORM_QKV_WIDTHS = frozenset({32, 64, 128})
 # From this width up the out-projection and FFN run as GEMMs + a separate LayerNorm.
 WIDE_GEMM_FROM = 256
+# GEMM-route width whose residual projections fuse the next LayerNorm (256 x 256 tiles).
+WIDE_LN_EPILOGUE_WIDTH = 256
 
 
 @dataclass(frozen=True)
@@ -61,6 +70,7 @@ class Route:
     fuse_attention_output_norm: bool = True
     fuse_full_ffn: bool = True
     fuse_layer_tail: bool = False
+    wide_ln_epilogue: bool = False
     qkv_variant: int = 0
     attention_variant: int = 0
     out_ln_variant: int = 0
@@ -81,6 +91,7 @@ class Route:
             "attention_output_norm_fusion": self.fuse_attention_output_norm,
             "full_ffn_fusion": self.fuse_full_ffn,
             "layer_tail_fusion": self.fuse_layer_tail,
+            "wide_ln_epilogue": self.wide_ln_epilogue,
             "variants": {
                 "qkv": self.qkv_variant,
                 "attention": self.attention_variant,
@@ -137,6 +148,10 @@ def plan(
         fuse_out and fuse_ffn and enable_fp16_normalized_stream and enable_fp16_custom_attention
         and (d, f) in LAYER_TAIL_SHAPES and d in LAYERNORM_QKV_WIDTHS
     )
+    wide_ln = (
+        enable_attention_output_norm_fusion and enable_full_ffn_fusion and not narrow
+        and d == WIDE_LN_EPILOGUE_WIDTH
+    )
     route = Route(
         True,
         "hip",
@@ -145,6 +160,7 @@ def plan(
         fuse_attention_output_norm=fuse_out,
         fuse_full_ffn=fuse_ffn,
         fuse_layer_tail=fuse_tail,
+        wide_ln_epilogue=wide_ln,
     )
     tuned = TUNED.get((d, f, h, _token_bucket(int(config.batch_size) * int(config.seq_len))))
     if tuned:

@@ -193,6 +193,58 @@ def mixed_linear_add_layer_norm(
     return residual_out, normalized_out
 
 
+WIDE_LN_EPILOGUE_WIDTH = 256
+
+
+def mixed_linear_residual_layer_norm(
+    x: torch.Tensor,
+    linear: nn.Linear,
+    residual: torch.Tensor,
+    norm: nn.LayerNorm,
+    *,
+    normalized_dtype: torch.dtype = torch.float32,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``R' = fp16(x) @ W^T + b + residual``; ``N' = LayerNorm(R')`` for any input width.
+
+    The wide-route counterpart of ``mixed_linear_add_layer_norm`` (whose
+    projection is square): the out-projection or the FFN-output projection,
+    its residual add and the next LayerNorm (reference generic route,
+    ``mixed_precision/transformer.py:664-690``) run as one kernel on 256 x 256
+    GEMM tiles.  ``linear.out_features`` must be 256.  Returns ``(R', N')``.
+    """
+    n_features = linear.out_features
+    if not (
+        _gpu(x)
+        and x.dtype in (torch.float16, torch.float32)
+        and _gpu(residual)
+        and residual.dtype == torch.float32
+        and x.shape[:-1] == residual.shape[:-1]
+        and x.shape[-1] == linear.in_features
+        and linear.in_features % 8 == 0
+        and residual.shape[-1] == n_features == WIDE_LN_EPILOGUE_WIDTH
+        and _fp16_linear_ok(linear)
+        and _norm_ok(norm, n_features)
+        and normalized_dtype in (torch.float16, torch.float32)
+    ):
+        raise ValueError("unsupported projection/residual/LayerNorm inputs")
+    n_rows = residual.numel() // n_features
+    residual_out = torch.empty_like(residual)
+    normalized_out = torch.empty_like(residual, dtype=normalized_dtype)
+    if not _aligned(x, residual, linear.weight, linear.bias, norm.weight, norm.bias, residual_out, normalized_out):
+        raise ValueError("unsupported projection/residual/LayerNorm inputs (16-byte alignment)")
+    lib = _lib.load()
+    _lib.check(
+        lib.mpk_linear_add_layernorm(
+            x.data_ptr(), _lib.dtype_code(x.dtype), linear.weight.data_ptr(), linear.bias.data_ptr(),
+            residual.data_ptr(), norm.weight.data_ptr(), norm.bias.data_ptr(), residual_out.data_ptr(),
+            normalized_out.data_ptr(), _lib.dtype_code(normalized_dtype), n_rows, n_features,
+            linear.in_features, float(norm.eps), _lib.stream_handle(x.device),
+        ),
+        "mpk_linear_add_layernorm",
+    )
+    return residual_out, normalized_out
+
+
 def mixed_ffn_add_layer_norm(
     x: torch.Tensor,
     linear_in: nn.Linear,

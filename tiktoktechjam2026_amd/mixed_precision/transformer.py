@@ -23,6 +23,9 @@ Routes (chosen by ``dispatch.plan`` from the shape):
   out-projection with the residual add in its epilogue (mpk_linear_residual),
   LayerNorm (mpk_layernorm), FFN-in + GELU (mpk_linear), FFN-out + residual
   (mpk_linear_residual) and the next LayerNorm, on large persistent GEMM tiles.
+  At d_model 256 the two residual projections also carry the LayerNorm that
+  follows them (mpk_linear_add_layernorm), so the route has no LayerNorm
+  launch after the first.
 
 The last two routes start with one LayerNorm.  The last layer's normalized output is FP32 (it is
 the model output).  Rounding points: GEMM operands FP16, accumulation / bias /
@@ -47,6 +50,7 @@ from .hip_linear import (
     mixed_linear,
     mixed_linear_add_layer_norm,
     mixed_linear_residual,
+    mixed_linear_residual_layer_norm,
 )
 
 
@@ -104,6 +108,10 @@ class MixedPrecisionSelfAttention(nn.Module):
                     ctx, self.out_proj, residual_fp32, next_norm,
                     normalized_dtype=route.normalized_dtype, variant=route.out_ln_variant,
                 )
+            if route.wide_ln_epilogue:
+                return mixed_linear_residual_layer_norm(
+                    ctx, self.out_proj, residual_fp32, next_norm, normalized_dtype=route.normalized_dtype
+                )
             x = mixed_linear_residual(ctx, self.out_proj, residual_fp32, variant=route.out_proj_variant)
             return x, layer_norm(x, next_norm, normalized_dtype=route.normalized_dtype)
         return mixed_linear(ctx, self.out_proj, output_dtype=torch.float32)
@@ -139,6 +147,10 @@ class MixedPrecisionTransformerBlock(nn.Module):
         activated = mixed_linear(
             normalized_ffn, self.ffn_in, output_dtype=torch.float16, fuse_gelu=True, variant=route.ffn_in_variant
         )
+        if route.wide_ln_epilogue:
+            return mixed_linear_residual_layer_norm(
+                activated, self.ffn_out, residual, next_norm, normalized_dtype=out_dtype
+            )
         if self.ffn_out.in_features == self.ffn_out.out_features and route.fuse_attention_output_norm:
             return mixed_linear_add_layer_norm(
                 activated, self.ffn_out, residual, next_norm, normalized_dtype=out_dtype, variant=route.out_ln_variant

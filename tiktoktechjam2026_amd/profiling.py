@@ -81,13 +81,21 @@ def forward_costs(config, normalized_bytes: int = 2, route=None) -> Dict[str, Ke
                 M * D * (2 + 4 + 4 + 4) + 2.0 * (D * D + 2 * D * F),
             ),
         }
-    norm_launches = 1 + (0 if route.fuse_attention_output_norm else L) + (0 if route.fuse_full_ffn else L)
+    wide_ln = getattr(route, "wide_ln_epilogue", False)
+    norm_launches = 1 if wide_ln else (
+        1 + (0 if route.fuse_attention_output_norm else L) + (0 if route.fuse_full_ffn else L)
+    )
     costs = {
         "layernorm": KernelCost("layernorm", norm_launches, 0.0, M * D * (4 + sn)),
         "qkv_proj": KernelCost("qkv_proj", L, 2.0 * M * 3 * D * D, M * D * sn + 3 * D * D * 2 + 3 * D * 2 + M * 3 * D * 2),
         "attention": attention,
     }
-    if route.fuse_attention_output_norm:
+    if wide_ln:
+        # residual projections with the next LayerNorm in the epilogue (256 x 256 GEMM tiles)
+        costs["out_proj_ln"] = KernelCost(
+            "out_proj_ln", L, 2.0 * M * D * D, M * D * 2 + 2 * D * D + 2 * D + 8 * M * D + M * D * sn + 8 * D
+        )
+    elif route.fuse_attention_output_norm:
         costs["out_proj_ln"] = KernelCost(
             "out_proj_ln", L, 2.0 * M * D * D, M * D * 2 + 2 * D * D + 8 * M * D + M * D * sn + 16 * D
         )
@@ -97,6 +105,12 @@ def forward_costs(config, normalized_bytes: int = 2, route=None) -> Dict[str, Ke
         )
     if route.fuse_full_ffn:
         costs["ffn_ln"] = KernelCost("ffn_ln", L, 4.0 * M * D * F, M * D * sn + 4 * D * F + M * D * (8 + sn))
+    elif wide_ln:
+        costs["ffn_in"] = KernelCost("ffn_in", L, 2.0 * M * D * F, M * D * sn + 2 * D * F + 2 * F + M * F * 2)
+        # the last layer's normalized output is FP32 (counted at the stream width here)
+        costs["ffn_out_ln"] = KernelCost(
+            "ffn_out_ln", L, 2.0 * M * D * F, M * F * 2 + 2 * D * F + 2 * D + 8 * M * D + M * D * sn + 8 * D
+        )
     else:
         costs["ffn_in"] = KernelCost("ffn_in", L, 2.0 * M * D * F, M * D * sn + 2 * D * F + 2 * F + M * F * 2)
         costs["ffn_out_residual"] = KernelCost(
@@ -161,6 +175,7 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
     from .mixed_precision.hip_fused import fused_layer_tail, layer_norm_qkv
     from .mixed_precision.hip_linear import (
         layer_norm, mixed_ffn_add_layer_norm, mixed_linear, mixed_linear_add_layer_norm, mixed_linear_residual,
+        mixed_linear_residual_layer_norm,
     )
 
     import dataclasses
@@ -193,7 +208,10 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
             qkv = mixed_linear(normalized, att.qkv_proj, output_dtype=torch.float16, variant=route.qkv_variant)
             q, k, v = qkv.view(B, S, 3, att.num_heads, att.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
             ctx = attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant).view(B, S, D)
-            if route.fuse_attention_output_norm:
+            if route.wide_ln_epilogue:
+                resid, nffn = mixed_linear_residual_layer_norm(ctx, att.out_proj, x, layer.norm2,
+                                                               normalized_dtype=sdt)
+            elif route.fuse_attention_output_norm:
                 resid, nffn = mixed_linear_add_layer_norm(ctx, att.out_proj, x, layer.norm2, normalized_dtype=sdt,
                                                           variant=route.out_ln_variant)
             else:
@@ -206,8 +224,12 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
                 "qkv_proj": lambda: mixed_linear(normalized, att.qkv_proj, output_dtype=torch.float16,
                                                  variant=route.qkv_variant),
                 "attention": lambda: attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant),
-                "out_proj_ln": lambda: mixed_linear_add_layer_norm(ctx, att.out_proj, x, layer.norm2,
-                                                                   normalized_dtype=sdt, variant=route.out_ln_variant),
+                "out_proj_ln": (
+                    (lambda: mixed_linear_residual_layer_norm(ctx, att.out_proj, x, layer.norm2, normalized_dtype=sdt))
+                    if route.wide_ln_epilogue else
+                    (lambda: mixed_linear_add_layer_norm(ctx, att.out_proj, x, layer.norm2, normalized_dtype=sdt,
+                                                         variant=route.out_ln_variant))
+                ),
                 "out_proj_residual": lambda: mixed_linear_residual(ctx, att.out_proj, x,
                                                                    variant=route.out_proj_variant),
                 "ffn_ln": lambda: mixed_ffn_add_layer_norm(nffn, layer.ffn_in, layer.ffn_out, resid, layer.norm1,
@@ -216,6 +238,8 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
                                                variant=route.ffn_in_variant),
                 "ffn_out_residual": lambda: mixed_linear_residual(hidden, layer.ffn_out, resid,
                                                                   variant=route.ffn_out_variant),
+                "ffn_out_ln": lambda: mixed_linear_residual_layer_norm(hidden, layer.ffn_out, resid, layer.norm1,
+                                                                       normalized_dtype=sdt),
             }
         rows = []
         for name, fn in launches.items():
