@@ -275,7 +275,9 @@ def describe_rate(value: float) -> str:
 _KERNEL_KEYS = (
     ("layer_tail_kernel<128, 32, 1, false", "layernorm_qkv"),
     ("layer_tail_kernel", "layer_tail"),
+    ("attention32_kernel", "attention"),
     ("attention_kernel", "attention"),
+    ("linear_big_kernel", "linear"),
     ("linear_kernel", "linear"),
     ("ffn_ln_kernel", "ffn_ln"),
     ("residual_layernorm_kernel", "layernorm"),
