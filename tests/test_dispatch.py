@@ -20,6 +20,22 @@ def test_benchmark_config_routes():
         assert route.normalized_dtype == torch.float16
 
 
+def test_wide_layernorm_epilogue_route():
+    """d_model 256 (cfg5): the residual GEMMs carry the next LayerNorm; other widths and
+    disabled fusions keep the separate LayerNorm launches."""
+    flags = {name: dispatch.plan(cfg).wide_ln_epilogue for name, cfg in BENCHMARK_CONFIGS.items()}
+    assert flags == {"cfg1": False, "cfg2": False, "cfg3": False, "cfg4": False, "cfg5": True}
+    cfg5 = BENCHMARK_CONFIGS["cfg5"]
+    assert not dispatch.plan(cfg5, enable_attention_output_norm_fusion=False).wide_ln_epilogue
+    assert not dispatch.plan(cfg5, enable_full_ffn_fusion=False).wide_ln_epilogue
+    from tiktoktechjam2026_amd import profiling
+
+    costs = profiling.forward_costs(cfg5, 2, dispatch.plan(cfg5))
+    assert costs["layernorm"].launches_per_forward == 1
+    assert {"out_proj_ln", "ffn_in", "ffn_out_ln"} <= set(costs)
+    assert "ffn_out_residual" not in costs and "out_proj_residual" not in costs
+
+
 def test_enable_flags_change_the_route():
     cfg = BENCHMARK_CONFIGS["cfg2"]
     assert not dispatch.plan(cfg, enable_full_ffn_fusion=False).fuse_layer_tail
