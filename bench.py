@@ -217,7 +217,7 @@ def main(argv=None) -> int:
                 t0 = time.perf_counter()
                 ref = strict_fp32.forward_in_slices(sample_x, oracle_state, config, slice_size=1)
                 times.append(time.perf_counter() - t0)
-                if time.perf_counter() - t_budget >= args.cpu_seconds or len(times) >= 50:
+                if time.perf_counter() - t_budget >= args.cpu_seconds or len(times) >= 1000:
                     break
         timed = times[1:] if len(times) > 1 else times
         cpu_median = statistics.median(timed)

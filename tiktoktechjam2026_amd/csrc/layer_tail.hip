@@ -236,8 +236,6 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
     // rows of this wave / workgroup that exist (stores to the others are dropped by the buffer resource)
     const uint32_t wrows = (uint32_t)(M - m0 <= 0 ? 0 : (M - m0 < 16 * TM ? M - m0 : 16 * TM));
     const uint32_t grows = (uint32_t)(M - wg0 < ROWS ? M - wg0 : ROWS);
-    TileIn<D, TM, STAGE1> nxt;
-    if (tile + gridDim.x < ntiles) load_tile<D, TM, STAGE1>(nxt, a, (tile + gridDim.x) * ROWS + wave * 16 * TM, r, g);
 
     // xr: the residual stream of this wave's rows (lane holds row m0+16t+r, features 32p+8g+j)
     float xr[TM][PN][8];
@@ -374,6 +372,13 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
         }
       }
     }
+
+    // The next tile's inputs are requested here, once this tile's residual rows
+    // are dead: prefetched from the start of the tile they would hold 48+
+    // registers through the out-projection and FFN, where the weight fragments
+    // need them to keep LDS reads ahead of the MFMAs.
+    TileIn<D, TM, STAGE1> nxt;
+    if (tile + gridDim.x < ntiles) load_tile<D, TM, STAGE1>(nxt, a, (tile + gridDim.x) * ROWS + wave * 16 * TM, r, g);
 
     if constexpr (QKV && QMODE == kQkvLds) {
       _Float16* qkv = static_cast<_Float16*>(a.out);
