@@ -157,24 +157,35 @@ __device__ __forceinline__ void store8(_Float16* p, const float* v) {
   *reinterpret_cast<h8*>(p) = h;
 }
 
-// Exact (erf-based) GELU in FP32: 0.5 v (1 + erf(v / sqrt(2))).
 // Exact-erf GELU, x * Phi(x) = 0.5 x (1 + erf(x / sqrt 2)), in FP32.  erf comes from
 // Abramowitz & Stegun, Handbook of Mathematical Functions, formula 7.1.26:
 //   erf(z) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),  t = 1 / (1 + p z),  z >= 0,
-// |error| <= 1.5e-7 for all z (about one FP32 ulp of 1).  Over x in [-12, 12] the GELU
-// differs from the float64 value by at most 4.2e-7, the same size as the rounding error
-// of evaluating 0.5 x (1 + erff(x / sqrt 2)) in FP32 (4.5e-7), at about a third of the
-// instructions of the library erff (one reciprocal, one exp2, 13 other VALU operations).
-// The coefficients below are the handbook's a_i halved, so q = erfc(|x| / sqrt 2) / 2.
+// |error| <= 1.5e-7 for all z (about one FP32 ulp of 1).  With the a_i halved,
+// q = (a1 t + ... + a5 t^5) exp(-z^2) is erfc(|x| / sqrt 2) / 2 = Phi(-|x|), and
+//   GELU(x) = x (1 - q) for x >= 0,  x q for x < 0,  i.e.  max(x, 0) - |x| q
+// (one FMA).  The variable is u = z sqrt(log2 e), so exp(-z^2) = exp2(-u u) and
+// p becomes p / sqrt(log2 e).  Per element: one reciprocal, one exp2 and 11 other
+// VALU operations.  Over x in [-12, 12] the result differs from the float64 GELU
+// by at most 3.4e-7 (FP32 emulation of these steps), below the rounding error of
+// evaluating 0.5 x (1 + erff(x / sqrt 2)) in FP32 (4.5e-7).
 __device__ __forceinline__ float gelu_erf(float x) {
-  constexpr float kP = 0.3275911f;
+  constexpr float kU = 0.84932180028801904f;  // sqrt(log2 e) / sqrt 2
+  constexpr float kP = 0.2727374808792225f;   // 0.3275911 / sqrt(log2 e)
   constexpr float kA1 = 0.5f * 0.254829592f, kA2 = 0.5f * -0.284496736f, kA3 = 0.5f * 1.421413741f;
   constexpr float kA4 = 0.5f * -1.453152027f, kA5 = 0.5f * 1.061405429f;
-  const float z = fabsf(x) * 0.70710678118654752f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(kP, z, 1.0f));
+  const float ax = fabsf(x);
+  const float u = ax * kU;
+  const float t = __builtin_amdgcn_rcpf(fmaf(u, kP, 1.0f));
   const float poly = t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, kA5, kA4), kA3), kA2), kA1);
-  const float q = poly * __builtin_amdgcn_exp2f(z * (z * -1.4426950408889634f));
-  return x * (x >= 0.f ? 1.0f - q : q);
+  const float q = poly * __builtin_amdgcn_exp2f(-(u * u));
+  float r = fmaf(-ax, q, fmaxf(x, 0.0f));
+  // r is rounded to FP32 here.  A caller's FP16 conversion then rounds that value, as
+  // the reference's FP32 GELU followed by a cast does; without the (empty) asm the
+  // compiler may fuse the FMA and the conversion into v_fma_mix, which rounds the
+  // unrounded result once - in some kernels and not in others, so identical rows
+  // would get different FP16 hidden activations depending on the tile shape.
+  __asm__("" : "+v"(r));
+  return r;
 }
 
 // Reductions over the four lane groups g that share one MFMA column (lanes l,
