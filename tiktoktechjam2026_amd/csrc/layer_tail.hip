@@ -374,9 +374,8 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
     }
 
     // The next tile's inputs are requested here, once this tile's residual rows
-    // are dead: prefetched from the start of the tile they would hold 48+
-    // registers through the out-projection and FFN, where the weight fragments
-    // need them to keep LDS reads ahead of the MFMAs.
+    // are dead, so that their 48+ registers are not held through the
+    // out-projection and FFN stages; the QKV stage still covers the load latency.
     TileIn<D, TM, STAGE1> nxt;
     if (tile + gridDim.x < ntiles) load_tile<D, TM, STAGE1>(nxt, a, (tile + gridDim.x) * ROWS + wave * 16 * TM, r, g);
 
