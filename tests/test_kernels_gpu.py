@@ -128,6 +128,36 @@ def test_mixed_linear(hip_device, m, n, k, variant):
                 _close(y, ref, tol, tol, f"linear in={in_dtype} out={out_dtype} gelu={gelu}")
 
 
+@pytest.mark.parametrize("n,variant", [(8, 0), (256, 7), (128, 1)])
+def test_gelu_epilogue_accuracy(hip_device, n, variant):
+    """The GEMM's GELU alone: X = [v, 0, ...] and W[:, 0] = 1 make every pre-activation
+    exactly the FP16 value v, so the FP32 output is the kernel's GELU(v).  Every FP16 value
+    in [-16, 16] plus large magnitudes, against float64 exact-erf GELU."""
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear
+
+    bits = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16)
+    v = bits.view(torch.float16)
+    v = v[torch.isfinite(v) & (v.abs() <= 16)]
+    v = torch.cat([v, torch.tensor([-65504.0, -100.0, -30.0, -20.0, 20.0, 30.0, 100.0, 65504.0]).half()])
+    k = 8
+    x = torch.zeros(v.numel(), k, dtype=torch.float16)
+    x[:, 0] = v
+    lin = torch.nn.Linear(k, n).to(hip_device).half()
+    with torch.no_grad():
+        lin.weight.zero_()
+        lin.weight[:, 0] = 1.0
+        lin.bias.zero_()
+    y = mixed_linear(x.to(hip_device), lin, output_dtype=torch.float32, fuse_gelu=True, variant=variant)
+    vd = v.double()
+    ref = 0.5 * vd * (1.0 + torch.erf(vd / math.sqrt(2.0)))
+    err = (y.cpu().double() - ref[:, None]).abs()
+    assert torch.isfinite(y).all()
+    # A&S 7.1.26 erf (|error| <= 1.5e-7) plus FP32 rounding: below 1e-6 absolute where
+    # |GELU| < 1 and 1e-6 relative above
+    scaled = err / ref.abs().clamp_min(1.0)[:, None]
+    assert float(scaled.max()) <= 1e-6, f"max scaled err {float(scaled.max()):.3g} at v={float(v[scaled.max(1).values.argmax()])}"
+
+
 @pytest.mark.parametrize(
     "m,n,k", [(8192, 512, 2048), (777, 256, 256), (3, 136, 40), (70000, 128, 512), (4100, 1024, 264)]
 )
