@@ -249,14 +249,20 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
         for (int p = 0; p < PN; ++p) acc[p][0] = acc[p][1] = zero4();
 #pragma unroll
         for (int p = 0; p < PN; ++p) {
+          // all weight fragments of the feature pair are read before its MFMAs, so one
+          // LDS latency covers the group instead of one per MFMA
+          h8 w[KS][2];
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-              const h8 w = *reinterpret_cast<const h8*>(
+            for (int tt = 0; tt < 2; ++tt)
+              w[ks][tt] = *reinterpret_cast<const h8*>(
                   &lds[SH::WO + (32 * p + pair_row(r, tt)) * SH::LDD + ks * 32 + 8 * g]);
-              acc[p][tt] = mfma32(w, cur.ctx[t][ks], acc[p][tt]);
-            }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) acc[p][tt] = mfma32(w[ks][tt], cur.ctx[t][ks], acc[p][tt]);
           __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
@@ -293,15 +299,22 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
         f4 hacc[TM][2];
 #pragma unroll
         for (int t = 0; t < TM; ++t) hacc[t][0] = hacc[t][1] = zero4();
+        // Win fragments of this feature pair, read as a group before its MFMAs
+        h8 wi[KS][2];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-          for (int tt = 0; tt < 2; ++tt) {
-            const h8 w = *reinterpret_cast<const h8*>(
+          for (int tt = 0; tt < 2; ++tt)
+            wi[ks][tt] = *reinterpret_cast<const h8*>(
                 &lds[SH::WIN + (32 * fq + pair_row(r, tt)) * SH::LDD + ks * 32 + 8 * g]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int t = 0; t < TM; ++t) hacc[t][tt] = mfma32(w, n2f[t][ks], hacc[t][tt]);
-          }
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int t = 0; t < TM; ++t) hacc[t][tt] = mfma32(wi[ks][tt], n2f[t][ks], hacc[t][tt]);
+        __builtin_amdgcn_sched_barrier(0);
         float bi[8];
         lds8(prm + SH::P_BIN + 32 * fq + 8 * g, bi);
         h8 hb[TM];
@@ -312,15 +325,21 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
             hb[t][i] = (_Float16)gelu_erf(hacc[t][0][i] + bi[i]);
             hb[t][4 + i] = (_Float16)gelu_erf(hacc[t][1][i] + bi[4 + i]);
           }
+        // Wout fragments of this hidden pair, read as a group before its MFMAs
+        h8 wo[PN][2];
 #pragma unroll
         for (int p = 0; p < PN; ++p)
 #pragma unroll
-          for (int tt = 0; tt < 2; ++tt) {
-            const h8 w = *reinterpret_cast<const h8*>(
+          for (int tt = 0; tt < 2; ++tt)
+            wo[p][tt] = *reinterpret_cast<const h8*>(
                 &lds[SH::WOUT + (32 * p + pair_row(r, tt)) * SH::LDF + 32 * fq + 8 * g]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int t = 0; t < TM; ++t) yacc[t][p][tt] = mfma32(w, hb[t], yacc[t][p][tt]);
-          }
+        for (int p = 0; p < PN; ++p)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int t = 0; t < TM; ++t) yacc[t][p][tt] = mfma32(wo[p][tt], hb[t], yacc[t][p][tt]);
         __builtin_amdgcn_sched_barrier(0);
       }
       const __amdgpu_buffer_rsrc_t xres = make_rsrc(a.x_out + m0 * D, wrows * (uint32_t)(D * 4));
