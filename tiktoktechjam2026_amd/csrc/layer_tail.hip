@@ -248,21 +248,21 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
 #pragma unroll
         for (int p = 0; p < PN; ++p) acc[p][0] = acc[p][1] = zero4();
 #pragma unroll
-        for (int p = 0; p < PN; ++p) {
-          // all weight fragments of the feature pair are read before its MFMAs, so one
-          // LDS latency covers the group instead of one per MFMA
-          h8 w[KS][2];
+        for (int ks = 0; ks < KS; ++ks) {
+          // the weight fragments of one k-step for every output pair are read before its
+          // MFMAs (one LDS latency per group), which then feed 2 PN independent chains
+          h8 w[PN][2];
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
+          for (int p = 0; p < PN; ++p)
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
-              w[ks][tt] = *reinterpret_cast<const h8*>(
+              w[p][tt] = *reinterpret_cast<const h8*>(
                   &lds[SH::WO + (32 * p + pair_row(r, tt)) * SH::LDD + ks * 32 + 8 * g]);
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
+          for (int p = 0; p < PN; ++p)
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) acc[p][tt] = mfma32(w[ks][tt], cur.ctx[t][ks], acc[p][tt]);
+            for (int tt = 0; tt < 2; ++tt) acc[p][tt] = mfma32(w[p][tt], cur.ctx[t][ks], acc[p][tt]);
           __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
