@@ -247,6 +247,10 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
         f4 acc[PN][2];
 #pragma unroll
         for (int p = 0; p < PN; ++p) acc[p][0] = acc[p][1] = zero4();
+        // the bias is requested ahead of the products, so its LDS latency is hidden by them
+        float bv[PN][8];
+#pragma unroll
+        for (int p = 0; p < PN; ++p) lds8(prm + SH::P_BO + 32 * p + 8 * g, bv[p]);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           // the weight fragments of one k-step for every output pair are read before its
@@ -267,25 +271,26 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
         }
 #pragma unroll
         for (int p = 0; p < PN; ++p) {
-          float bv[8];
-          lds8(prm + SH::P_BO + 32 * p + 8 * g, bv);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            xr[t][p][i] = (acc[p][0][i] + bv[i]) + cur.x[t][p][i];
-            xr[t][p][4 + i] = (acc[p][1][i] + bv[4 + i]) + cur.x[t][p][4 + i];
+            xr[t][p][i] = (acc[p][0][i] + bv[p][i]) + cur.x[t][p][i];
+            xr[t][p][4 + i] = (acc[p][1][i] + bv[p][4 + i]) + cur.x[t][p][4 + i];
           }
+        }
+        // LN2's gamma and beta are requested before the row statistics, which hide their latency
+        float gm[PN][8], bt[PN][8];
+#pragma unroll
+        for (int p = 0; p < PN; ++p) {
+          lds8(prm + SH::P_G2 + 32 * p + 8 * g, gm[p]);
+          lds8(prm + SH::P_BE2 + 32 * p + 8 * g, bt[p]);
         }
         float mean, rstd;
         row_stats<PN>(xr[t], inv_d, a.eps2, mean, rstd);
 #pragma unroll
-        for (int p = 0; p < PN; ++p) {
-          const int n = 32 * p + 8 * g;
-          float gm[8], bt[8];
-          lds8(prm + SH::P_G2 + n, gm);
-          lds8(prm + SH::P_BE2 + n, bt);
+        for (int p = 0; p < PN; ++p)
 #pragma unroll
-          for (int j = 0; j < 8; ++j) n2f[t][p][j] = (_Float16)((xr[t][p][j] - mean) * rstd * gm[j] + bt[j]);
-        }
+          for (int j = 0; j < 8; ++j)
+            n2f[t][p][j] = (_Float16)((xr[t][p][j] - mean) * rstd * gm[p][j] + bt[p][j]);
       }
 
       // ---- FFN: x'' = x' + Wout fp16(GELU(Win n2 + bin)) + bout ----
@@ -299,6 +304,8 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
         f4 hacc[TM][2];
 #pragma unroll
         for (int t = 0; t < TM; ++t) hacc[t][0] = hacc[t][1] = zero4();
+        float bi[8];  // requested first: the FFN-in products below hide its latency
+        lds8(prm + SH::P_BIN + 32 * fq + 8 * g, bi);
         // Win fragments of this feature pair, read as a group before its MFMAs
         h8 wi[KS][2];
 #pragma unroll
@@ -315,8 +322,6 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
 #pragma unroll
             for (int t = 0; t < TM; ++t) hacc[t][tt] = mfma32(wi[ks][tt], n2f[t][ks], hacc[t][tt]);
         __builtin_amdgcn_sched_barrier(0);
-        float bi[8];
-        lds8(prm + SH::P_BIN + 32 * fq + 8 * g, bi);
         h8 hb[TM];
 #pragma unroll
         for (int t = 0; t < TM; ++t)
@@ -343,17 +348,18 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
         __builtin_amdgcn_sched_barrier(0);
       }
       const __amdgpu_buffer_rsrc_t xres = make_rsrc(a.x_out + m0 * D, wrows * (uint32_t)(D * 4));
+      float bo2[PN][8];  // all of b_out in one group of LDS reads
+#pragma unroll
+      for (int p = 0; p < PN; ++p) lds8(prm + SH::P_BOUT + 32 * p + 8 * g, bo2[p]);
 #pragma unroll
       for (int t = 0; t < TM; ++t) {
 #pragma unroll
         for (int p = 0; p < PN; ++p) {
           const int n = 32 * p + 8 * g;
-          float bv[8];
-          lds8(prm + SH::P_BOUT + n, bv);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            xr[t][p][i] = (yacc[t][p][0][i] + bv[i]) + xr[t][p][i];
-            xr[t][p][4 + i] = (yacc[t][p][1][i] + bv[4 + i]) + xr[t][p][4 + i];
+            xr[t][p][i] = (yacc[t][p][0][i] + bo2[p][i]) + xr[t][p][i];
+            xr[t][p][4 + i] = (yacc[t][p][1][i] + bo2[p][4 + i]) + xr[t][p][4 + i];
           }
           buffer_store8(xres, (uint32_t)((16 * t + r) * D + n) * 4u, xr[t][p], a.x_out);
         }
@@ -373,16 +379,21 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
                                                   LAST ? wrows * (uint32_t)(D * 4) : 0u);
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
+      // gamma and beta are requested before the row statistics, which hide their latency
+      float gm[PN][8], bt[PN][8];
+#pragma unroll
+      for (int p = 0; p < PN; ++p) {
+        lds8(prm + SH::P_G1 + 32 * p + 8 * g, gm[p]);
+        lds8(prm + SH::P_BE1 + 32 * p + 8 * g, bt[p]);
+      }
       float mean, rstd;
       row_stats<PN>(xr[t], inv_d, a.eps1, mean, rstd);
 #pragma unroll
       for (int p = 0; p < PN; ++p) {
         const int n = 32 * p + 8 * g;
-        float gm[8], bt[8], o[8];
-        lds8(prm + SH::P_G1 + n, gm);
-        lds8(prm + SH::P_BE1 + n, bt);
+        float o[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = (xr[t][p][j] - mean) * rstd * gm[j] + bt[j];
+        for (int j = 0; j < 8; ++j) o[j] = (xr[t][p][j] - mean) * rstd * gm[p][j] + bt[p][j];
         if constexpr (LAST) {
           buffer_store8(ores, (uint32_t)((16 * t + r) * D + n) * 4u, o, static_cast<float*>(a.out));
         } else {
