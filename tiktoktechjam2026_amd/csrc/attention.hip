@@ -506,7 +506,10 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
   static_assert(KTILE % 32 == 0 && KTILE <= NT, "key tile");
 
   __shared__ _Float16 ks_lds[2][SH::KBUF];
-  __shared__ _Float16 vt_lds[2][SH::VBUF];
+  // V is staged row-major like K (one 16-byte store per chunk); the P V product
+  // reads its V^T fragments with LDS transpose loads (ds_read_b64_tr_b16)
+  constexpr int LDVR = SH::LDK;
+  __shared__ _Float16 vr_lds[2][KTILE * LDVR];
   __shared__ float kbias[2][KTILE];
 
   const int S = a.seq;
@@ -573,8 +576,8 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
   const int kv_end = a.causal ? min(q0 + QB, S) : S;
   const int ntiles = (kv_end + KTILE - 1) / KTILE;
 
-  // ---- register prefetch / LDS staging of one K/V tile (as in attention_kernel) ----
-  h8 kreg[SH::PER_THREAD], vreg[SH::V_PER_THREAD][2];
+  // ---- register prefetch / LDS staging of one K/V tile (both row-major) ----
+  h8 kreg[SH::PER_THREAD], vreg[SH::PER_THREAD];
   float breg = 0.f;
   const uint32_t krow_bytes = (uint32_t)(a.ks[2] * (int64_t)sizeof(IT));
   const uint32_t vrow_bytes = (uint32_t)(a.vs[2] * (int64_t)sizeof(IT));
@@ -589,14 +592,10 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
       if (cc < SH::CHUNKS) kreg[i] = buffer_load8_as_half(kr, key * krow_bytes + col * (uint32_t)sizeof(IT), Kp);
     }
 #pragma unroll
-    for (int i = 0; i < SH::V_PER_THREAD; ++i) {
+    for (int i = 0; i < SH::PER_THREAD; ++i) {
       const int cc = threadIdx.x + i * NT;
-      const int kp = cc % (KTILE / 2), col = (cc / (KTILE / 2)) * 8;
-      if (cc < SH::VITEMS) {
-        const uint32_t off = 2 * kp * vrow_bytes + col * (uint32_t)sizeof(IT);
-        vreg[i][0] = buffer_load8_as_half(vr, off, Vp);
-        vreg[i][1] = buffer_load8_as_half(vr, off + vrow_bytes, Vp);
-      }
+      const int key = cc / SH::CPK, col = (cc % SH::CPK) * 8;
+      if (cc < SH::CHUNKS) vreg[i] = buffer_load8_as_half(vr, key * vrow_bytes + col * (uint32_t)sizeof(IT), Vp);
     }
     if (threadIdx.x < KTILE) {
       const int gk = kb + threadIdx.x;
@@ -612,24 +611,33 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
       if (cc < SH::CHUNKS) {
         const int key = cc / SH::CPK, col = (cc % SH::CPK) * 8;
         *reinterpret_cast<h8*>(&ks_lds[buf][key * SH::LDK + col]) = kreg[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < SH::V_PER_THREAD; ++i) {
-      const int cc = threadIdx.x + i * NT;
-      if (cc < SH::VITEMS) {
-        const int kp = cc % (KTILE / 2), col = (cc / (KTILE / 2)) * 8;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-          h2 pair;
-          pair[0] = vreg[i][0][j];
-          pair[1] = vreg[i][1][j];
-          *reinterpret_cast<h2*>(&vt_lds[buf][(col + j) * SH::LDV + 2 * kp]) = pair;
-        }
+        *reinterpret_cast<h8*>(&vr_lds[buf][key * LDVR + col]) = vreg[i];
       }
     }
     if (threadIdx.x < KTILE) kbias[buf][threadIdx.x] = breg;
+  };
+  // V^T fragment (A operand of O^T = V^T P^T) from the row-major V tile: MFMA row i
+  // (head dim 32 dt + kappa(i)) and keys k0 .. k0 + 7, as two transpose loads.  Within
+  // each 16-lane group a transpose load hands lane j element (j % 4) of the 8 bytes read
+  // by lane 4 m + j / 4, for m = 0..3; so lane r of group G reads key k0 + r / 4 (+4) at
+  // the 4 dims starting at 32 dt + 16 (G & 1) + 8 (q & 1) + 4 (q >> 1), q = r % 4, and
+  // every lane receives 4 consecutive keys of its own row's dim.
+  typedef short s4v __attribute__((ext_vector_type(4)));
+  const int vtr_r = l & 15, vtr_g = l >> 4, vtr_q = vtr_r & 3;
+  const int vtr_dim = 16 * (vtr_g & 1) + 8 * (vtr_q & 1) + 4 * (vtr_q >> 1);
+  auto vt_frag = [&](const _Float16* vrb, int dt, int k0) {
+    const _Float16* p0 = vrb + (k0 + (vtr_r >> 2)) * LDVR + 32 * dt + vtr_dim;
+    const s4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4v*)(p0));
+    const s4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4v*)(p0 + 4 * LDVR));
+    typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+    const h4v a = __builtin_bit_cast(h4v, lo), b = __builtin_bit_cast(h4v, hi);
+    h8 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = a[j];
+      v[4 + j] = b[j];
+    }
+    return v;
   };
 
   // ---- one key tile ----
@@ -731,7 +739,7 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-          const h8 va = *reinterpret_cast<const h8*>(&vtb[(32 * dt + trow) * SH::LDV + 32 * nb + 16 * s2 + 8 * hf]);
+          const h8 va = vt_frag(vtb, dt, 32 * nb + 16 * s2 + 8 * hf);
           oacc[dt] = mfma32x32(va, pf[s2], oacc[dt]);
         }
     }
@@ -748,7 +756,7 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
     const int kb = tile * KTILE;
     const bool more = tile + 1 < ntiles;
     if (more) fetch(kb + KTILE);
-    process(kb, ks_lds[cur], vt_lds[cur], kbias[cur], first_tag, edge_tag);
+    process(kb, ks_lds[cur], vr_lds[cur], kbias[cur], first_tag, edge_tag);
     if (more) stash(cur ^ 1);
     __syncthreads();
   };
