@@ -105,6 +105,11 @@ def test_auto_variant_queries(built_library):
     assert lib.mpk_linear_residual_layernorm_auto_variant(262144, 256) == 3
     assert lib.mpk_ffn_residual_layernorm_auto_variant(65536, 128, 128) in (1, 2)
     assert lib.mpk_attention_auto_variant(64, 4, 1024, 32) in range(1, 9)
+    # short sequences stay on the 16x16 kernel; from 256 keys hd 32 / 64 use the 32x32 one
+    assert lib.mpk_attention_auto_variant(64, 4, 128, 32) == 1
+    assert lib.mpk_attention_auto_variant(64, 4, 256, 32) == 6
+    assert lib.mpk_attention_auto_variant(64, 4, 256, 64) == 7
+    assert lib.mpk_attention_auto_variant(16, 8, 2048, 64) == 6
     # the 32x32 kernel variants (6..8) only for head_dim 32 / 64
     for hd in (8, 16, 128, 256):
         for s in (128, 1024, 4096):
