@@ -92,22 +92,46 @@ struct TailShape {
   static constexpr int BYTES = PARAM_OFF * 2 + NPARAM * 4;
 };
 
-// Copy a [rows, cols] FP16 matrix (row-major, cols % 8 == 0) into LDS with row stride ld.
-__device__ __forceinline__ void stage_matrix(_Float16* dst, const _Float16* src, int rows, int cols, int ld) {
-  const int cpr = cols / 8;
-  for (int c = threadIdx.x; c < rows * cpr; c += kTailThreads) {
-    const int row = c / cpr, col = (c % cpr) * 8;
-    *reinterpret_cast<h8*>(&dst[row * ld + col]) = *reinterpret_cast<const h8*>(&src[(int64_t)row * cols + col]);
+// Two-phase staging of a [ROWS, COLS] FP16 matrix into LDS (row stride LD): load()
+// issues all of this thread's global reads, store() writes them to LDS, so the
+// reads of every staged array can be in flight together.
+template <int ROWS, int COLS, int LD, bool ON>
+struct MatStage {
+  static constexpr int CPR = COLS / 8;
+  static constexpr int CHUNKS = ON ? ROWS * CPR : 0;
+  static constexpr int PER = ON ? (CHUNKS + kTailThreads - 1) / kTailThreads : 1;
+  h8 v[PER];
+  __device__ __forceinline__ void load(const _Float16* src) {
+    if constexpr (ON) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int c = threadIdx.x + i * kTailThreads;
+        if (c < CHUNKS) v[i] = *reinterpret_cast<const h8*>(&src[(int64_t)(c / CPR) * COLS + (c % CPR) * 8]);
+      }
+    }
   }
-}
+  __device__ __forceinline__ void store(_Float16* dst) const {
+    if constexpr (ON) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int c = threadIdx.x + i * kTailThreads;
+        if (c < CHUNKS) *reinterpret_cast<h8*>(&dst[(c / CPR) * LD + (c % CPR) * 8]) = v[i];
+      }
+    }
+  }
+};
 
-// Copy n FP16 (as_half) or FP32 parameters into the FP32 LDS parameter block.
-__device__ __forceinline__ void stage_params(float* dst, const _Float16* src, int n) {
-  for (int i = threadIdx.x; i < n; i += kTailThreads) dst[i] = (float)src[i];
-}
-__device__ __forceinline__ void stage_params(float* dst, const float* src, int n) {
-  for (int i = threadIdx.x; i < n; i += kTailThreads) dst[i] = src[i];
-}
+// Two-phase staging of n (1 <= n <= kTailThreads) FP16 or FP32 parameters as FP32.
+// The read is unconditional (threads past n re-read element n - 1), so no
+// branch separates it from the other prologue reads.
+template <typename T>
+struct ParamStage {
+  T v;
+  __device__ __forceinline__ void load(const T* src, int n) { v = src[min((int)threadIdx.x, n - 1)]; }
+  __device__ __forceinline__ void store(float* dst, int n) const {
+    if ((int)threadIdx.x < n) dst[threadIdx.x] = (float)v;
+  }
+};
 
 // 8 consecutive FP32 parameters from LDS.
 __device__ __forceinline__ void lds8(const float* p, float* v) {
@@ -192,26 +216,32 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
   const int l = threadIdx.x & 63, wave = wave_id();
   const int r = l & 15, g = l >> 4;
 
-  if constexpr (STAGE1) {
-    stage_matrix(lds + SH::WO, a.wo, D, D, SH::LDD);
-    stage_matrix(lds + SH::WIN, a.win, F, D, SH::LDD);
-    stage_matrix(lds + SH::WOUT, a.wout, D, F, SH::LDF);
-  }
-  if constexpr (QKV && QMODE == kQkvLds) stage_matrix(lds + SH::WQKV, a.wqkv, 3 * D, D, SH::LDD);
+  // Prologue: every global read (weights, parameters, the register-resident QKV
+  // weights) is issued before the first LDS write, so it costs one memory latency.
+  static_assert(3 * D <= kTailThreads && F <= kTailThreads, "one parameter per thread");
+  MatStage<D, D, SH::LDD, STAGE1> s_wo;
+  MatStage<F, D, SH::LDD, STAGE1> s_win;
+  MatStage<D, F, SH::LDF, STAGE1> s_wout;
+  MatStage<3 * D, D, SH::LDD, QKV && QMODE == kQkvLds> s_wqkv;
   // Biases, gammas and betas live in LDS for the whole kernel: read inside the
   // per-tile dependency chain, global loads would put a memory latency between
   // every product and its epilogue.
-  float* prm = reinterpret_cast<float*>(lds + SH::PARAM_OFF);
+  ParamStage<_Float16> p_bo, p_bin, p_bout, p_bqkv;
+  ParamStage<float> p_g2, p_be2, p_g1, p_be1;
   if constexpr (STAGE1) {
-    stage_params(prm + SH::P_BO, a.bo, D);
-    stage_params(prm + SH::P_G2, a.g2, D);
-    stage_params(prm + SH::P_BE2, a.be2, D);
-    stage_params(prm + SH::P_BIN, a.bin, F);
-    stage_params(prm + SH::P_BOUT, a.bout, D);
+    p_bo.load(a.bo, D);
+    p_g2.load(a.g2, D);
+    p_be2.load(a.be2, D);
+    p_bin.load(a.bin, F);
+    p_bout.load(a.bout, D);
   }
-  stage_params(prm + SH::P_G1, a.g1, D);
-  stage_params(prm + SH::P_BE1, a.be1, D);
-  if constexpr (QKV) stage_params(prm + SH::P_BQKV, a.bqkv, 3 * D);
+  p_g1.load(a.g1, D);
+  p_be1.load(a.be1, D);
+  if constexpr (QKV) p_bqkv.load(a.bqkv, 3 * D);
+  s_wo.load(a.wo);
+  s_win.load(a.win);
+  s_wout.load(a.wout);
+  s_wqkv.load(a.wqkv);
   h8 wq[QKV && QMODE == kQkvReg ? QNT : 1][KS];
   if constexpr (QKV && QMODE == kQkvReg) {
 #pragma unroll
@@ -220,6 +250,21 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
       for (int ks = 0; ks < KS; ++ks)
         wq[nt][ks] = *reinterpret_cast<const h8*>(a.wqkv + (int64_t)(QNW * wave + 16 * nt + r) * D + ks * 32 + 8 * g);
   }
+  float* prm = reinterpret_cast<float*>(lds + SH::PARAM_OFF);
+  if constexpr (STAGE1) {
+    p_bo.store(prm + SH::P_BO, D);
+    p_g2.store(prm + SH::P_G2, D);
+    p_be2.store(prm + SH::P_BE2, D);
+    p_bin.store(prm + SH::P_BIN, F);
+    p_bout.store(prm + SH::P_BOUT, D);
+  }
+  p_g1.store(prm + SH::P_G1, D);
+  p_be1.store(prm + SH::P_BE1, D);
+  if constexpr (QKV) p_bqkv.store(prm + SH::P_BQKV, 3 * D);
+  s_wo.store(lds + SH::WO);
+  s_win.store(lds + SH::WIN);
+  s_wout.store(lds + SH::WOUT);
+  s_wqkv.store(lds + SH::WQKV);
   __syncthreads();
 
   const float inv_d = 1.0f / (float)D;
