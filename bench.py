@@ -96,8 +96,8 @@ def main(argv=None) -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(
-            "bench.py measures one MI355X: this build has no multi-GPU path (batch sharding needs no "
-            "collective in the forward; see DESIGN.md). Run with --gpus 1.",
+            "bench.py measures one MI355X: this build has no multi-GPU path (sharding the batch "
+            "across GPUs needs no collective in the forward). Run with --gpus 1.",
             file=sys.stderr,
         )
         return 2
@@ -261,7 +261,7 @@ def main(argv=None) -> int:
             round(value / PUBLISHED_TOKENS_PER_S[args.config], 3) if args.config in PUBLISHED_TOKENS_PER_S else None
         ),
         "vs_baseline_ref": (
-            "reference candidate's published tokens/s on RTX 5060 Laptop (BASELINE.md)"
+            "reference candidate's published tokens/s on RTX 5060 Laptop"
             if args.config in PUBLISHED_TOKENS_PER_S else None
         ),
         "dtype": "fp16",
