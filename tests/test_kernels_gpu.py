@@ -506,6 +506,20 @@ def test_layer_norm_qkv(hip_device, d, m, variant):
 @pytest.mark.parametrize("last", [False, True])
 @pytest.mark.parametrize("variant", [1, 2])
 def test_fused_layer_tail(hip_device, d, f, m, last, variant):
+    _check_layer_tail(hip_device, d, f, m, last, variant)
+
+
+# Row counts that give every workgroup of the persistent grid at least two tiles, with a
+# ragged last tile on the second pass (d 32/64: 512 workgroups x 128 rows; d 128: 256 x 128).
+@pytest.mark.parametrize("d,f,m", [(32, 64, 2 * 512 * 128 + 37), (64, 256, 2 * 512 * 128 + 37),
+                                   (128, 128, 2 * 256 * 128 + 37)])
+@pytest.mark.parametrize("last", [False, True])
+@pytest.mark.parametrize("variant", [1, 2])
+def test_fused_layer_tail_multi_pass(hip_device, d, f, m, last, variant):
+    _check_layer_tail(hip_device, d, f, m, last, variant)
+
+
+def _check_layer_tail(hip_device, d, f, m, last, variant):
     from tiktoktechjam2026_amd.mixed_precision.hip_fused import fused_layer_tail
 
     ctx = _randn((m, d), 61)

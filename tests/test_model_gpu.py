@@ -119,8 +119,18 @@ def test_long_sequence_case14_prefix_property(hip_device):
     assert torch.equal(out[:, :2048], head)
 
 
-def test_padded_input_matches_oracle(hip_device):
-    config = TransformerConfig(4, 96, 128, 4, 128, 2, True)
+PADDED_CASES = [
+    TransformerConfig(4, 96, 128, 4, 128, 2, True),   # layer-tail route
+    TransformerConfig(3, 160, 256, 8, 512, 2, True),  # GEMM route, LayerNorm in the residual GEMMs
+    TransformerConfig(2, 130, 512, 8, 1024, 2, True),  # GEMM route, d_model 512
+    TransformerConfig(3, 100, 256, 4, 256, 2, False),  # non-causal: valid queries see every valid key
+]
+
+
+@pytest.mark.parametrize("config", PADDED_CASES, ids=[f"d{c.d_model}{'' if c.causal else '_noncausal'}"
+                                                      for c in PADDED_CASES])
+def test_padded_input_matches_oracle(hip_device, config):
+    print(f"\n[padded] config={config}", flush=True)
     state = strict_fp32.seeded_state_dict(config, 99)
     model = MixedPrecisionTransformer(config)
     copy_mixed_model_weights(state, model)
@@ -132,8 +142,24 @@ def test_padded_input_matches_oracle(hip_device):
         out = model(x.to(hip_device), mask.to(hip_device)).cpu()
         ref = strict_fp32.forward(x, state, config, mask)
     result = harness.compare_outputs(ref, out, rtol=RTOL, atol=ATOL)
+    print(f"[padded] max_abs={result.max_abs_error:.6g} failed={result.failed_elements}", flush=True)
     assert result.failed_elements == 0, result
     assert torch.count_nonzero(out[~mask]) == 0
+
+
+def test_strided_input_view(hip_device):
+    """A non-contiguous FP32 view is accepted like the reference module accepts it."""
+    config = TransformerConfig(4, 96, 128, 4, 128, 2, True)
+    state, model = _build(config, hip_device)
+    g = torch.Generator().manual_seed(17)
+    base = torch.randn(config.seq_len, config.batch_size, config.d_model, generator=g)
+    x = base.to(hip_device).transpose(0, 1)  # [B, S, D] view, not contiguous
+    assert not x.is_contiguous()
+    with torch.inference_mode():
+        out = model(x).cpu()
+        ref = strict_fp32.forward(base.transpose(0, 1).contiguous(), state, config)
+    result = harness.compare_outputs(ref, out, rtol=RTOL, atol=ATOL)
+    assert result.failed_elements == 0, result
 
 
 def test_causality_and_batch_independence_exact(hip_device):

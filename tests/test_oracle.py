@@ -10,6 +10,7 @@
 
 from __future__ import annotations
 
+import dataclasses
 import json
 import math
 import os
@@ -74,8 +75,12 @@ def test_seeded_weights_match_reference_fingerprints(fingerprints, name):
         assert math.isclose(float((flat * flat).sum()), fp["sumsq"], rel_tol=1e-9), key
 
 
-def _brute_force_forward(x, state, config):
-    """Float64 per-query restatement with explicit loops over heads and queries."""
+def _brute_force_forward(x, state, config, mask=None):
+    """Float64 per-query restatement with explicit loops over heads and queries.
+
+    ``mask`` (bool ``[B, S]``, True = valid) removes padded keys from every
+    query's softmax; padded rows of the attention output, of every layer's
+    residual stream and of the final output are zero."""
     x = x.double()
     st = {k: v.double() for k, v in state.items()}
     d, h = config.d_model, config.num_heads
@@ -99,15 +104,25 @@ def _brute_force_forward(x, state, config):
                 sl = slice(head * hd, (head + 1) * hd)
                 for t in range(x.shape[1]):
                     keys = range(t + 1) if config.causal else range(x.shape[1])
+                    if mask is not None:
+                        keys = [j for j in keys if bool(mask[b, j])]
+                        if not keys or not bool(mask[b, t]):
+                            continue  # padded query: its row is zeroed below
                     s = torch.stack([q[b, t, sl] @ k[b, j, sl] for j in keys]) / math.sqrt(hd)
                     w = torch.exp(s - s.max())
                     w = w / w.sum()
                     ctx[b, t, sl] = sum(w[i] * v[b, j, sl] for i, j in enumerate(keys))
-        x = x + lin(ctx, p + "attention.out_proj")
+        attn = lin(ctx, p + "attention.out_proj")
+        if mask is not None:
+            attn = attn * mask[..., None]
+        x = x + attn
         hid = lin(ln(x, p + "norm2"), p + "ffn_in")
         hid = 0.5 * hid * (1 + torch.erf(hid / math.sqrt(2)))
         x = x + lin(hid, p + "ffn_out")
-    return ln(x, "final_norm")
+        if mask is not None:
+            x = x * mask[..., None]
+    out = ln(x, "final_norm")
+    return out if mask is None else out * mask[..., None]
 
 
 @pytest.mark.parametrize("name", sorted(TINY))
@@ -160,6 +175,43 @@ def test_oracle_padding_mask_zeroes_rows():
     out = strict_fp32.forward(x, state, config, mask)
     assert torch.count_nonzero(out[~mask]) == 0
     assert torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_oracle_padded_prefix_equals_truncated_sequence(causal):
+    """With prefix masks, a padded sequence's valid prefix is the forward of the truncated
+    sequence.  The padded positions hold large non-zero inputs, so a key mask applied on the
+    wrong side (queries instead of keys) or not at all changes the non-causal result."""
+    config = TransformerConfig(3, 20, 32, 4, 48, 2, causal)
+    state = strict_fp32.seeded_state_dict(config, 21)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 20, 32, generator=g)
+    lengths = [20, 13, 6]
+    mask = torch.arange(20)[None, :] < torch.tensor(lengths)[:, None]
+    x = torch.where(mask[..., None], x, 25.0 * torch.randn(3, 20, 32, generator=g))
+    out = strict_fp32.forward(x, state, config, mask)
+    for b, n in enumerate(lengths):
+        alone = strict_fp32.forward(x[b:b + 1, :n], state, dataclasses.replace(config, batch_size=1, seq_len=n))
+        assert torch.allclose(out[b, :n], alone[0], atol=2e-5), (b, n)
+        assert torch.count_nonzero(out[b, n:]) == 0
+    if not causal:
+        # the same forward without the mask lets valid queries see the padded keys
+        unmasked = strict_fp32.forward(x, state, config)
+        assert not torch.allclose(unmasked[1, :13], out[1, :13], atol=1e-3)
+
+
+def test_oracle_arbitrary_key_mask_matches_brute_force():
+    """A non-prefix key mask (holes inside the sequence) against the float64 per-query loop."""
+    config = TransformerConfig(2, 12, 16, 2, 24, 2, False)
+    state = strict_fp32.seeded_state_dict(config, 8)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(2, 12, 16, generator=g)
+    mask = torch.ones(2, 12, dtype=torch.bool)
+    mask[0, [2, 3, 7]] = False
+    mask[1, [0, 11]] = False
+    got = strict_fp32.forward(x, state, config, mask)
+    ref = _brute_force_forward(x, state, config, mask)
+    assert torch.allclose(got.double(), ref, atol=2e-5, rtol=0), float((got.double() - ref).abs().max())
 
 
 def test_input_generator_pins_cpu_rng():

@@ -1,0 +1,96 @@
+"""CPU tests of the rocprofv3 summary helpers: kernel-name parsing, per-dispatch labelling of the
+projection roles, and the counter arithmetic on hand-made CSV files."""
+
+from __future__ import annotations
+
+import csv
+import json
+
+import pytest
+
+from tiktoktechjam2026_amd import profiling
+
+BIG_LN = "_ZN3mpk17linear_big_kernelILi256ELi2EDF16_Li4EDF16_EEvNS_10LinearArgsE"
+BIG_RES = "_ZN3mpk17linear_big_kernelILi256ELi2EDF16_Li3EfEEvNS_10LinearArgsE"
+BIG_QKV = "_ZN3mpk17linear_big_kernelILi256ELi2EfLi0EDF16_EEvNS_10LinearArgsE"
+BIG_GELU = "_ZN3mpk17linear_big_kernelILi256ELi2EDF16_Li1EDF16_EEvNS_10LinearArgsE"
+ATTN = "_ZN3mpk18attention32_kernelILi32ELi8ELi64EDF16_DF16_Lb0EEEvNS_8AttnArgsE"
+TAIL = "_ZN3mpk17layer_tail_kernelILi128ELi128ELi1ELb1ELb0ELi1EEEvNS_8TailArgsE"
+TAIL_LAST = "_ZN3mpk17layer_tail_kernelILi128ELi128ELi1ELb1ELb1ELi1EEEvNS_8TailArgsE"
+HEAD = "_ZN3mpk17layer_tail_kernelILi128ELi32ELi1ELb0ELb0ELi1EEEvNS_8TailArgsE"
+COPY = "__amd_rocclr_copyBuffer"
+
+
+def test_parse_mangled_and_demangled_names():
+    assert profiling.parse_kernel_name(BIG_LN) == ("linear_big_kernel", ["256", "2", "_Float16", "4", "_Float16"])
+    assert profiling.parse_kernel_name(ATTN)[1][-1] == "false"
+    assert profiling.parse_kernel_name("void mpk::linear_big_kernel<256, 2, float, 0, _Float16>(mpk::LinearArgs)") == (
+        "linear_big_kernel", ["256", "2", "float", "0", "_Float16"])
+    keys = [profiling.base_kernel_key(n) for n in (BIG_QKV, BIG_GELU, BIG_RES, BIG_LN, ATTN, TAIL, TAIL_LAST, HEAD)]
+    assert keys == ["qkv_proj", "ffn_in", "@residual", "@ln", "attention", "layer_tail", "layer_tail_last",
+                    "layernorm_qkv"]
+
+
+def test_label_dispatches_separates_out_projection_from_ffn_output():
+    forward = [BIG_QKV, ATTN, BIG_LN, BIG_GELU, BIG_LN] * 2
+    assert profiling.label_dispatches(forward) == ["qkv_proj", "attention", "out_proj_ln", "ffn_in", "ffn_out_ln"] * 2
+    # per-kernel timing loops: each kernel repeated, in forward order
+    loops = [ATTN] * 3 + [BIG_RES] * 3 + [BIG_GELU] * 3 + [BIG_RES] * 3
+    assert profiling.label_dispatches(loops)[3:6] == ["out_proj_residual"] * 3
+    assert profiling.label_dispatches(loops)[9:] == ["ffn_out_residual"] * 3
+
+
+def _write_counters(path, dispatches):
+    fields = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+    with open(path, "w", newline="") as handle:
+        writer = csv.DictWriter(handle, fieldnames=fields)
+        writer.writeheader()
+        for i, (name, counters, ns) in enumerate(dispatches, start=1):
+            for counter, value in counters.items():
+                writer.writerow({"Dispatch_Id": i, "Kernel_Name": name, "Counter_Name": counter,
+                                 "Counter_Value": value, "Start_Timestamp": 1000, "End_Timestamp": 1000 + ns})
+
+
+def test_traffic_summary_scales_by_the_calibration_copy(tmp_path):
+    gib_kib = (1 << 30) / 1024
+    fetch = tmp_path / "fetch.csv"
+    write = tmp_path / "write.csv"
+    # FETCH_SIZE reads half of the copy's bytes, WRITE_SIZE all of them
+    _write_counters(fetch, [(COPY, {"FETCH_SIZE": gib_kib / 2}, 10), (ATTN, {"FETCH_SIZE": 1000.0}, 10),
+                            (ATTN, {"FETCH_SIZE": 3000.0}, 10)])
+    _write_counters(write, [(COPY, {"WRITE_SIZE": gib_kib}, 10), (ATTN, {"WRITE_SIZE": 500.0}, 10),
+                            (ATTN, {"WRITE_SIZE": 500.0}, 10)])
+    summary = profiling.traffic_summary(str(fetch), str(write))
+    assert summary["calibration"]["fetch_scale"] == pytest.approx(2.0)
+    row = summary["kernels"]["attention"]
+    assert row["fetch_bytes"] == pytest.approx(2000.0 * 1024 * 2.0)
+    assert row["write_bytes"] == pytest.approx(500.0 * 1024)
+    assert "copy" not in summary["kernels"]
+
+
+def test_mfma_summary_busy_fraction_and_rate(tmp_path):
+    counters = tmp_path / "mfma.csv"
+    trace = tmp_path / "trace.csv"
+    _write_counters(counters, [(ATTN, {"SQ_VALU_MFMA_BUSY_CYCLES": 512.0 * 1000, "GRBM_GUI_ACTIVE": 1000.0,
+                                       "SQ_INSTS_VALU_MFMA_MOPS_F16": 1e6}, 5000)])
+    with open(trace, "w", newline="") as handle:
+        writer = csv.DictWriter(handle, fieldnames=["Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        writer.writeheader()
+        writer.writerow({"Dispatch_Id": 1, "Kernel_Name": ATTN, "Start_Timestamp": 0, "End_Timestamp": 2000})
+    row = profiling.mfma_summary(str(counters), str(trace))["attention"]
+    assert row["mfma_busy"] == pytest.approx(0.5)  # 512k busy SIMD-cycles over 1000 cycles x 1024 SIMDs
+    assert row["mfma_flops_per_launch"] == pytest.approx(512e6)
+    assert row["mfma_tflops"] == pytest.approx(512e6 / 2e-6 / 1e12)
+
+
+def test_parity_table_orders_records(tmp_path):
+    records = [
+        {"config": "cfg5", "trial": 0, "input_seed": 1234, "elements": 10, "failed": 0, "max_abs": 1e-3,
+         "max_rel": 0.01, "mean_abs": 1e-4, "gpu_vs_cpu_oracle_max_abs": 1e-6},
+        {"config": "cfg1", "trial": 1, "input_seed": 1235, "elements": 10, "failed": 0, "max_abs": 1e-3,
+         "max_rel": 0.01, "mean_abs": 1e-4, "gpu_vs_cpu_oracle_max_abs": None},
+    ]
+    path = tmp_path / "records.json"
+    path.write_text(json.dumps(records))
+    lines = profiling.parity_table(str(path)).splitlines()
+    assert lines[2].startswith("| cfg1 | 1 |") and lines[3].startswith("| cfg5 | 0 |")

@@ -873,13 +873,15 @@ static hipError_t attn_dispatch(int variant, const AttnArgs& a, int hd, hipStrea
 
 using namespace mpk;
 
-// Built-in choice, from MI355X sweeps: short sequences favour 16 queries per wave
-// (more workgroups); from 512 keys on, head dims 32 and 64 run the 32x32 kernel
-// (4-wave workgroups with 64-key tiles, 8-wave workgroups for head_dim 32 at
-// S >= 4096), other head dims 32 queries per wave and 8-wave workgroups at S >= 4096.
+// Built-in choice, from MI355X sweeps.  Below 256 keys, and for head dims 128 and
+// 256, the 16x16 kernel with 16 queries per wave (variant 1: most workgroups).
+// From 256 keys on, head dims 32 and 64 run the 32x32 kernel: 4-wave workgroups
+// with 64-key tiles (variant 6), except 8-wave workgroups (variant 7) for
+// head_dim 32 at S >= 4096 and for head_dim 64 below 1024 keys.  Head dims 8 and
+// 16 take 32 queries per wave from 512 keys (variant 2) and 8-wave workgroups
+// from 4096 keys (variant 4).
 extern "C" int mpk_attention_auto_variant(int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim) {
   (void)batch; (void)heads;
-  // measured on MI355X: the 32x32 kernel wins from 256 keys on (hd 64: 8 waves below 1024)
   if (head_dim >= 128 || seq_len < 256) return 1;
   if (head_dim == 32) return seq_len >= 4096 ? 7 : 6;
   if (head_dim == 64) return seq_len < 1024 ? 7 : 6;

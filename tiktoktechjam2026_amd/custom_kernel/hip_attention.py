@@ -23,12 +23,14 @@ from typing import Optional
 
 import torch
 
-from .. import _lib
+from .. import _ops
+from .._lib import F16, F32
 
 HEAD_DIMS = (8, 16, 32, 64, 128, 256)
 
 
-def _common_ok(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dtype: torch.dtype) -> bool:
+def _layout_ok(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dtype: torch.dtype) -> bool:
+    """Device, dtype, shape and stride checks (what ``torch.compile`` can trace)."""
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         return False
     if not (q.dtype == k.dtype == v.dtype == dtype):
@@ -41,9 +43,13 @@ def _common_ok(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dtype: torch.d
         return False
     esz = q.element_size()
     for t in (q, k, v):
-        if t.data_ptr() % 16 != 0 or any((s * esz) % 16 != 0 for s in t.stride()[:3]):
+        if any((s * esz) % 16 != 0 for s in t.stride()[:3]):
             return False
     return True
+
+
+def _common_ok(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dtype: torch.dtype) -> bool:
+    return _layout_ok(q, k, v, dtype) and all(t.data_ptr() % 16 == 0 for t in (q, k, v))
 
 
 def is_supported(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool) -> bool:
@@ -72,7 +78,7 @@ def attention(
     ``key_valid`` is an optional bool ``[B, S]`` key-padding mask (True = may be
     attended).  ``out_dtype`` defaults to the input dtype.
     """
-    if not _common_ok(q, k, v, q.dtype) or q.dtype not in (torch.float16, torch.float32):
+    if not _layout_ok(q, k, v, q.dtype) or q.dtype not in (torch.float16, torch.float32):
         raise ValueError(f"unsupported custom-attention input: shape={tuple(q.shape)}, dtype={q.dtype}")
     batch, heads, seq_len, head_dim = q.shape
     out_dtype = q.dtype if out_dtype is None else out_dtype
@@ -83,21 +89,8 @@ def attention(
         if key_valid.shape != (batch, seq_len) or key_valid.device != q.device:
             raise ValueError("key_valid must be a [batch, seq_len] mask on the input device")
         mask_u8 = key_valid.to(torch.uint8).contiguous()
-    output = torch.empty((batch, seq_len, heads, head_dim), device=q.device, dtype=out_dtype)
-    # output viewed with the [B, H, S, hd] index order of the inputs
-    o_strides = (output.stride(0), output.stride(2), output.stride(1), output.stride(3))
-    lib = _lib.load()
-    _lib.check(
-        lib.mpk_causal_attention(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), output.data_ptr(), _lib.dtype_code(q.dtype),
-            _lib.dtype_code(out_dtype), _lib.strides4(q.stride()), _lib.strides4(k.stride()),
-            _lib.strides4(v.stride()), _lib.strides4(o_strides), batch, heads, seq_len, head_dim, float(scale),
-            1 if causal else 0, None if mask_u8 is None else mask_u8.data_ptr(), int(variant),
-            _lib.stream_handle(q.device),
-        ),
-        "mpk_causal_attention",
-    )
-    return output
+    return _ops.attention(q, k, v, mask_u8, float(scale), bool(causal), F16 if out_dtype == torch.float16 else F32,
+                          int(variant))
 
 
 def launch_causal_attention(

@@ -15,8 +15,9 @@ the shape is only
   weight for every 64-128 rows, while the GEMM tiles read it once per 256
   rows and keep the matrix cores busy, and
 * the kernel tile variant of each launch.  Variant 0 defers to the
-  library's built-in table (``mpk_*_auto_variant``); entries in ``TUNED``
-  override it for shapes measured on MI355X (256 CUs, 64-lane waves).
+  library's built-in table (``mpk_*_auto_variant``), which holds the choices
+  measured on MI355X (256 CUs, 64-lane waves); a ``Route`` can pin a variant
+  per launch (tests and sweeps do).
 
 At d_model 256 (``WIDE_LN_EPILOGUE_WIDTH``) the GEMM route's two residual
 projections carry the next LayerNorm in their epilogue (``wide_ln_epilogue``):
@@ -42,7 +43,7 @@ Tile variants (see the kernel sources for the exact tiles):
 
 from __future__ import annotations
 
-from dataclasses import dataclass, field, replace
+from dataclasses import dataclass, field
 from typing import Dict, Tuple
 
 import torch
@@ -106,18 +107,6 @@ class Route:
         }
 
 
-def _token_bucket(tokens: int) -> str:
-    if tokens < 16384:
-        return "small"
-    if tokens < 131072:
-        return "medium"
-    return "large"
-
-
-# (d_model, ffn_dim, num_heads, token bucket) -> variant overrides, from MI355X measurements.
-TUNED: Dict[Tuple[int, int, int, str], Dict[str, int]] = {}
-
-
 def plan(
     config,
     *,
@@ -162,7 +151,4 @@ def plan(
         fuse_layer_tail=fuse_tail,
         wide_ln_epilogue=wide_ln,
     )
-    tuned = TUNED.get((d, f, h, _token_bucket(int(config.batch_size) * int(config.seq_len))))
-    if tuned:
-        route = replace(route, **tuned)
     return route

@@ -6,7 +6,9 @@
 ``mixed_linear`` QKV projection (``mixed_precision/transformer.py:196-222,
 540-560, 88-120``), keeping every intermediate on chip.  ``layer_norm_qkv``
 fuses the initial ``norm1`` + cast (``:484-486``) with the first QKV projection.
-Both validate in Python (``ValueError``) and launch on torch's current stream.
+Both validate shapes, dtypes and layouts in Python (``ValueError``) and call
+one ``torch.library`` custom operator (``tiktoktechjam2026_amd/_ops.py``) that
+launches on torch's current stream.
 """
 
 from __future__ import annotations
@@ -16,16 +18,19 @@ from typing import Optional, Tuple
 import torch
 import torch.nn as nn
 
-from .. import _lib
-from .hip_linear import _aligned, _fp16_linear_ok, _gpu, _norm_ok
+from .. import _ops
+from ..dispatch import LAYER_TAIL_SHAPES, LAYERNORM_QKV_WIDTHS
+from .hip_linear import _fp16_linear_ok, _gpu, _norm_ok
 
 
 def layer_tail_supported(d_model: int, ffn_dim: int) -> bool:
-    return bool(_lib.load().mpk_layer_tail_supported(int(d_model), int(ffn_dim)))
+    """(d_model, ffn_dim) pairs the layer-tail kernel is built for (``mpk_layer_tail_supported``)."""
+    return (int(d_model), int(ffn_dim)) in LAYER_TAIL_SHAPES
 
 
 def layer_norm_qkv_supported(d_model: int) -> bool:
-    return bool(_lib.load().mpk_layernorm_qkv_supported(int(d_model)))
+    """d_model values of the LayerNorm + QKV kernel (``mpk_layernorm_qkv_supported``)."""
+    return int(d_model) in LAYERNORM_QKV_WIDTHS
 
 
 def layer_norm_qkv(x: torch.Tensor, norm: nn.LayerNorm, qkv_proj: nn.Linear, *, variant: int = 0) -> torch.Tensor:
@@ -41,20 +46,8 @@ def layer_norm_qkv(x: torch.Tensor, norm: nn.LayerNorm, qkv_proj: nn.Linear, *, 
         and layer_norm_qkv_supported(d)
     ):
         raise ValueError("unsupported LayerNorm/QKV inputs")
-    rows = x.numel() // d
-    out = torch.empty((*x.shape[:-1], 3 * d), device=x.device, dtype=torch.float16)
-    if not _aligned(x, norm.weight, norm.bias, qkv_proj.weight, qkv_proj.bias, out):
-        raise ValueError("unsupported LayerNorm/QKV inputs (16-byte alignment)")
-    lib = _lib.load()
-    _lib.check(
-        lib.mpk_layernorm_qkv(
-            x.data_ptr(), norm.weight.data_ptr(), norm.bias.data_ptr(), qkv_proj.weight.data_ptr(),
-            qkv_proj.bias.data_ptr(), out.data_ptr(), rows, d, float(norm.eps), int(variant),
-            _lib.stream_handle(x.device),
-        ),
-        "mpk_layernorm_qkv",
-    )
-    return out
+    return _ops.layer_norm_qkv(x, norm.weight, norm.bias, qkv_proj.weight, qkv_proj.bias, float(norm.eps),
+                               int(variant))
 
 
 def fused_layer_tail(
@@ -68,14 +61,12 @@ def fused_layer_tail(
     next_qkv_proj: Optional[nn.Linear] = None,
     *,
     variant: int = 0,
-    out: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Attention output projection through the next layer's QKV projection in one kernel.
 
     Returns ``(residual_out, qkv)`` with ``qkv`` FP16 ``[..., 3D]``, or, when
     ``next_qkv_proj`` is None (last layer), ``(residual_out, normalized)`` with
-    ``normalized = next_norm(residual_out)`` in FP32.  ``out`` optionally
-    supplies the second result's storage (e.g. a slice of a preallocated output).
+    ``normalized = next_norm(residual_out)`` in FP32.
     """
     d = ctx.shape[-1] if ctx.dim() else 0
     f = ffn_in.out_features
@@ -98,31 +89,9 @@ def fused_layer_tail(
         and layer_tail_supported(d, f)
     ):
         raise ValueError("unsupported fused layer-tail inputs")
-    rows = ctx.numel() // d
-    residual_out = torch.empty_like(residual)
-    shape = ctx.shape if last else (*ctx.shape[:-1], 3 * d)
-    dtype = torch.float32 if last else torch.float16
-    if out is None:
-        out = torch.empty(shape, device=ctx.device, dtype=dtype)
-    elif tuple(out.shape) != tuple(shape) or out.dtype != dtype or not _gpu(out):
-        raise ValueError("fused layer-tail `out` has the wrong shape, dtype or layout")
-    tensors = [ctx, residual, out_proj.weight, out_proj.bias, norm2.weight, norm2.bias, ffn_in.weight, ffn_in.bias,
-               ffn_out.weight, ffn_out.bias, next_norm.weight, next_norm.bias, residual_out, out]
-    if not last:
-        tensors += [next_qkv_proj.weight, next_qkv_proj.bias]
-    if not _aligned(*tensors):
-        raise ValueError("unsupported fused layer-tail inputs (16-byte alignment)")
-    lib = _lib.load()
-    _lib.check(
-        lib.mpk_layer_tail(
-            ctx.data_ptr(), residual.data_ptr(), out_proj.weight.data_ptr(), out_proj.bias.data_ptr(),
-            norm2.weight.data_ptr(), norm2.bias.data_ptr(), ffn_in.weight.data_ptr(), ffn_in.bias.data_ptr(),
-            ffn_out.weight.data_ptr(), ffn_out.bias.data_ptr(), next_norm.weight.data_ptr(),
-            next_norm.bias.data_ptr(), None if last else next_qkv_proj.weight.data_ptr(),
-            None if last else next_qkv_proj.bias.data_ptr(), residual_out.data_ptr(), out.data_ptr(),
-            1 if last else 0, rows, d, f, float(norm2.eps), float(next_norm.eps), int(variant),
-            _lib.stream_handle(ctx.device),
-        ),
-        "mpk_layer_tail",
+    tensors = [out_proj.weight, out_proj.bias, norm2.weight, norm2.bias, ffn_in.weight, ffn_in.bias,
+               ffn_out.weight, ffn_out.bias, next_norm.weight, next_norm.bias]
+    return _ops.layer_tail(
+        ctx, residual, tensors, None if last else next_qkv_proj.weight, None if last else next_qkv_proj.bias,
+        float(norm2.eps), float(next_norm.eps), int(variant),
     )
-    return residual_out, out

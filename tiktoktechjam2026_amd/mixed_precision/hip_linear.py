@@ -9,10 +9,13 @@ reference's ``mixed_precision/triton_linear.py`` (``mixed_linear`` :221,
 ``num_stages``) are accepted for call-site compatibility and ignored: tile
 shapes come from the HIP dispatch table, or from the extra ``variant`` keyword.
 
-Every wrapper validates its inputs in Python and raises ``ValueError`` before
-launching, allocates its outputs with ``torch.empty`` on the input device,
-and launches on torch's current HIP stream.  There is no CPU or PyTorch
-fallback: non-GPU tensors are rejected.
+Every wrapper validates shapes, dtypes and layouts in Python and raises
+``ValueError`` before launching, then calls one ``torch.library`` custom
+operator (``tiktoktechjam2026_amd/_ops.py``), which checks alignment,
+allocates the outputs with ``torch.empty`` on the input device and launches on
+torch's current HIP stream.  The validation reads only shapes, dtypes and
+strides, so ``torch.compile`` traces the wrappers into one graph of custom
+operators.  There is no CPU or PyTorch fallback: non-GPU tensors are rejected.
 """
 
 from __future__ import annotations
@@ -22,11 +25,12 @@ from typing import Optional, Tuple
 import torch
 import torch.nn as nn
 
-from .. import _lib
+from .. import _ops
+from .._lib import F16, F32
 
 
-def _aligned(*tensors: torch.Tensor) -> bool:
-    return all(t.data_ptr() % 16 == 0 for t in tensors)
+def _code(dtype: torch.dtype) -> int:
+    return F16 if dtype == torch.float16 else F32
 
 
 def _gpu(t: torch.Tensor) -> bool:
@@ -82,22 +86,7 @@ def mixed_linear(
         and linear.out_features % 8 == 0
     ):
         raise ValueError("unsupported mixed projection inputs")
-    in_features = linear.in_features
-    out_features = linear.out_features
-    n_rows = x.numel() // in_features
-    output = torch.empty((*x.shape[:-1], out_features), device=x.device, dtype=output_dtype)
-    if not _aligned(x, linear.weight, linear.bias, output):
-        raise ValueError("unsupported mixed projection inputs (16-byte alignment)")
-    lib = _lib.load()
-    _lib.check(
-        lib.mpk_linear(
-            x.data_ptr(), _lib.dtype_code(x.dtype), linear.weight.data_ptr(), linear.bias.data_ptr(),
-            output.data_ptr(), _lib.dtype_code(output_dtype), 1 if fuse_gelu else 0, n_rows, out_features,
-            in_features, int(variant), _lib.stream_handle(x.device),
-        ),
-        "mpk_linear",
-    )
-    return output
+    return _ops.linear(x, linear.weight, linear.bias, _code(output_dtype), bool(fuse_gelu), int(variant))
 
 
 def mixed_linear_residual(
@@ -127,20 +116,10 @@ def mixed_linear_residual(
                              and out.shape == residual.shape))
     ):
         raise ValueError("unsupported mixed projection/residual inputs")
-    n_rows = x.numel() // linear.in_features
-    output = torch.empty_like(residual) if out is None else out
-    if not _aligned(x, linear.weight, linear.bias, residual, output):
-        raise ValueError("unsupported mixed projection/residual inputs (16-byte alignment)")
-    lib = _lib.load()
-    _lib.check(
-        lib.mpk_linear_residual(
-            x.data_ptr(), _lib.dtype_code(x.dtype), linear.weight.data_ptr(), linear.bias.data_ptr(),
-            residual.data_ptr(), output.data_ptr(), n_rows, linear.out_features, linear.in_features, int(variant),
-            _lib.stream_handle(x.device),
-        ),
-        "mpk_linear_residual",
-    )
-    return output
+    if out is None:
+        return _ops.linear_residual(x, linear.weight, linear.bias, residual, int(variant))
+    _ops.linear_residual_into(x, linear.weight, linear.bias, residual, out, int(variant))
+    return out
 
 
 LN_FUSED_WIDTHS = (32, 64, 128, 256, 512)
@@ -174,23 +153,10 @@ def mixed_linear_add_layer_norm(
         and normalized_dtype in (torch.float16, torch.float32)
     ):
         raise ValueError("unsupported fused projection/residual/LayerNorm inputs")
-    n_features = x.shape[-1]
-    n_rows = x.numel() // n_features
-    residual_out = torch.empty_like(residual)
-    normalized_out = torch.empty_like(residual, dtype=normalized_dtype)
-    if not _aligned(x, residual, linear.weight, linear.bias, norm.weight, norm.bias, residual_out, normalized_out):
-        raise ValueError("unsupported fused projection/residual/LayerNorm inputs (16-byte alignment)")
-    lib = _lib.load()
-    _lib.check(
-        lib.mpk_linear_residual_layernorm(
-            x.data_ptr(), _lib.dtype_code(x.dtype), linear.weight.data_ptr(), linear.bias.data_ptr(),
-            residual.data_ptr(), norm.weight.data_ptr(), norm.bias.data_ptr(), residual_out.data_ptr(),
-            normalized_out.data_ptr(), _lib.dtype_code(normalized_dtype), n_rows, n_features, float(norm.eps),
-            int(variant), _lib.stream_handle(x.device),
-        ),
-        "mpk_linear_residual_layernorm",
+    return _ops.linear_residual_layer_norm(
+        x, linear.weight, linear.bias, residual, norm.weight, norm.bias, float(norm.eps), _code(normalized_dtype),
+        int(variant),
     )
-    return residual_out, normalized_out
 
 
 WIDE_LN_EPILOGUE_WIDTH = 256
@@ -227,22 +193,9 @@ def mixed_linear_residual_layer_norm(
         and normalized_dtype in (torch.float16, torch.float32)
     ):
         raise ValueError("unsupported projection/residual/LayerNorm inputs")
-    n_rows = residual.numel() // n_features
-    residual_out = torch.empty_like(residual)
-    normalized_out = torch.empty_like(residual, dtype=normalized_dtype)
-    if not _aligned(x, residual, linear.weight, linear.bias, norm.weight, norm.bias, residual_out, normalized_out):
-        raise ValueError("unsupported projection/residual/LayerNorm inputs (16-byte alignment)")
-    lib = _lib.load()
-    _lib.check(
-        lib.mpk_linear_add_layernorm(
-            x.data_ptr(), _lib.dtype_code(x.dtype), linear.weight.data_ptr(), linear.bias.data_ptr(),
-            residual.data_ptr(), norm.weight.data_ptr(), norm.bias.data_ptr(), residual_out.data_ptr(),
-            normalized_out.data_ptr(), _lib.dtype_code(normalized_dtype), n_rows, n_features,
-            linear.in_features, float(norm.eps), _lib.stream_handle(x.device),
-        ),
-        "mpk_linear_add_layernorm",
+    return _ops.linear_add_layer_norm(
+        x, linear.weight, linear.bias, residual, norm.weight, norm.bias, float(norm.eps), _code(normalized_dtype)
     )
-    return residual_out, normalized_out
 
 
 def mixed_ffn_add_layer_norm(
@@ -277,27 +230,10 @@ def mixed_ffn_add_layer_norm(
         and normalized_dtype in (torch.float16, torch.float32)
     ):
         raise ValueError("unsupported fused FFN inputs")
-    ffn_dim = linear_in.out_features
-    n_rows = x.numel() // d
-    residual_out = torch.empty_like(residual)
-    normalized_out = torch.empty_like(residual, dtype=normalized_dtype)
-    if not _aligned(
-        x, residual, linear_in.weight, linear_in.bias, linear_out.weight, linear_out.bias, norm.weight, norm.bias,
-        residual_out, normalized_out,
-    ):
-        raise ValueError("unsupported fused FFN inputs (16-byte alignment)")
-    lib = _lib.load()
-    _lib.check(
-        lib.mpk_ffn_residual_layernorm(
-            x.data_ptr(), _lib.dtype_code(x.dtype), linear_in.weight.data_ptr(), linear_in.bias.data_ptr(),
-            linear_out.weight.data_ptr(), linear_out.bias.data_ptr(), residual.data_ptr(), norm.weight.data_ptr(),
-            norm.bias.data_ptr(), residual_out.data_ptr(), normalized_out.data_ptr(),
-            _lib.dtype_code(normalized_dtype), n_rows, d, ffn_dim, float(norm.eps), int(variant),
-            _lib.stream_handle(x.device),
-        ),
-        "mpk_ffn_residual_layernorm",
+    return _ops.ffn_residual_layer_norm(
+        x, linear_in.weight, linear_in.bias, linear_out.weight, linear_out.bias, residual, norm.weight, norm.bias,
+        float(norm.eps), _code(normalized_dtype), int(variant),
     )
-    return residual_out, normalized_out
 
 
 def _add_layer_norm(
@@ -319,22 +255,9 @@ def _add_layer_norm(
         and _norm_ok(norm, width)
     ):
         raise ValueError(message)
-    n_rows = x.numel() // width
-    residual = torch.empty_like(x) if update is not None else None
-    normalized = torch.empty_like(x, dtype=normalized_dtype)
-    tensors = [x, norm.weight, norm.bias, normalized] + ([update, residual] if update is not None else [])
-    if not _aligned(*tensors):
-        raise ValueError(message + " (16-byte alignment)")
-    lib = _lib.load()
-    _lib.check(
-        lib.mpk_layernorm(
-            x.data_ptr(), None if update is None else update.data_ptr(), norm.weight.data_ptr(), norm.bias.data_ptr(),
-            None if residual is None else residual.data_ptr(), normalized.data_ptr(),
-            _lib.dtype_code(normalized_dtype), n_rows, width, float(norm.eps), _lib.stream_handle(x.device),
-        ),
-        "mpk_layernorm",
-    )
-    return residual, normalized
+    if update is None:
+        return None, _ops.layer_norm(x, norm.weight, norm.bias, float(norm.eps), _code(normalized_dtype))
+    return _ops.add_layer_norm(x, update, norm.weight, norm.bias, float(norm.eps), _code(normalized_dtype))
 
 
 def mixed_add_layer_norm(

@@ -212,17 +212,20 @@ class MixedPrecisionTransformer(nn.Module):
     def dispatch_report(self) -> Dict[str, object]:
         return self.route.describe()
 
-    def _forward_layer_tail(self, x: torch.Tensor, key_valid: Optional[torch.Tensor], causal: bool,
-                            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def _forward_layer_tail(self, x: torch.Tensor, key_valid: Optional[torch.Tensor], causal: bool) -> torch.Tensor:
         """1 + 2L launches: LayerNorm+QKV, then per layer attention and the fused layer tail."""
-        return _forward_layer_tail_impl(self, x, key_valid, causal, out)
+        return _forward_layer_tail_impl(self, x, key_valid, causal)
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         if x.dtype != torch.float32:
             raise ValueError("mixed candidate requires an FP32 input/residual stream")
         if not x.is_cuda:
             raise ValueError("the HIP forward requires a GPU input tensor")
+        # the reference module accepts any strided input; the kernels read rows densely
+        x = x.contiguous()
         effective_mask = None if self.assume_all_tokens_valid else valid_token_mask
+        if effective_mask is not None:
+            effective_mask = effective_mask.contiguous()
         causal = bool(self.config.causal)
         stream_dtype = self.route.normalized_dtype
         n_layers = len(self.layers)
@@ -247,7 +250,7 @@ class MixedPrecisionTransformer(nn.Module):
         return normalized
 
 
-def _forward_layer_tail_impl(model: "MixedPrecisionTransformer", x, key_valid, causal, out=None):
+def _forward_layer_tail_impl(model: "MixedPrecisionTransformer", x, key_valid, causal):
     route = model.route
     layers = model.layers
     qkv = layer_norm_qkv(x, layers[0].norm1, layers[0].attention.qkv_proj, variant=route.head_variant)
@@ -259,7 +262,7 @@ def _forward_layer_tail_impl(model: "MixedPrecisionTransformer", x, key_valid, c
         if last:
             x, result = fused_layer_tail(
                 ctx, x, att.out_proj, layer.norm2, layer.ffn_in, layer.ffn_out, model.final_norm, None,
-                variant=route.tail_variant, out=out,
+                variant=route.tail_variant,
             )
         else:
             nxt = layers[index + 1]

@@ -26,6 +26,8 @@ FLOPs / MFMA peak and bytes / HBM peak; ``frac`` is achieved / peak on that roof
 from __future__ import annotations
 
 import math
+import os
+import re
 from dataclasses import dataclass
 from typing import Callable, Dict, List
 
@@ -263,37 +265,106 @@ def describe_rate(value: float) -> str:
     return f"{value:,.0f}"
 
 
-# --------------------------------------------------------------------------- PMC traffic helpers
+# --------------------------------------------------------------------------- rocprofv3 summaries
 #
-#   python -m tiktoktechjam2026_amd.profiling run --config cfg2 --iters 3
-#       runs the configured forward eagerly (no graphs) for PMC collection, after a plain
-#       device copy of 1 GiB (the calibration kernel: 1 GiB read + 1 GiB written).
-#   python -m tiktoktechjam2026_amd.profiling summarize FETCH.csv WRITE.csv --config cfg2 --out J
-#       turns two rocprofv3 --pmc counter CSVs (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch)
-#       into HBM bytes per launch per kernel, each counter scaled by copy_bytes / counter(copy).
+# Every figure in the committed profile pages comes from these commands (run from the repository
+# root; the rocprofv3 output directories are written by the GPU runs):
+#
+#   python -m tiktoktechjam2026_amd.profiling run --config cfgN [--iters 3]
+#       the configured forward, eagerly (no graphs), for counter passes: first a plain 1 GiB
+#       device copy (the calibration kernel, 1 GiB read + 1 GiB written), then the forwards.
+#   python -m tiktoktechjam2026_amd.profiling traffic FETCH_DIR WRITE_DIR --config cfgN
+#       two `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of `run` -> HBM bytes per
+#       launch per kernel (KiB per dispatch, each counter scaled by the calibration copy's
+#       bytes / the counter's reading for it), merged into profiles/hbm_traffic.json.
+#   python -m tiktoktechjam2026_amd.profiling mfma MFMA_DIR TRACE_DIR --config cfgN
+#       one `rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 GRBM_GUI_ACTIVE
+#       SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA` run of `run`, plus the kernel trace of the
+#       bench command for durations -> MFMA busy fraction and counted MFMA FLOP/s per kernel,
+#       merged into profiles/mfma_counters.json.
+#   python -m tiktoktechjam2026_amd.profiling table RUNS_DIR
+#       bench lines RUNS_DIR/bench_cfgN.json, kernel traces RUNS_DIR/prof_cfgN/ and the two
+#       counter files -> profiles/forward_all_configs_mi355x.md.
+#   python -m tiktoktechjam2026_amd.profiling parity-table RECORDS.json
+#       whole-output parity records (tests/test_parity_full_gpu.py) ->
+#       profiles/parity_all_configs_mi355x.md.
 
-_KERNEL_KEYS = (
-    ("layer_tail_kernel<128, 32, 1, false", "layernorm_qkv"),
-    ("layer_tail_kernel", "layer_tail"),
-    ("attention32_kernel", "attention"),
-    ("attention_kernel", "attention"),
-    ("linear_big_kernel", "linear"),
-    ("linear_kernel", "linear"),
-    ("ffn_ln_kernel", "ffn_ln"),
-    ("residual_layernorm_kernel", "layernorm"),
-)
 CALIBRATION_BYTES = 1 << 30
+SIMD_PER_GPU = 1024  # MI355X: 256 CUs x 4 SIMDs (rocprofv3 agent info Simd_Count)
+
+_MANGLED_ARG = re.compile(r"Li(-?\d+)E|Lb([01])E|(DF16_)|(f)|(E)")
 
 
-def _kernel_key(name: str) -> str:
-    if "layer_tail_kernel" in name and ", true, true," in name:
-        return "layer_tail_last"
-    for pattern, key in _KERNEL_KEYS:
-        if pattern in name:
-            return key
+def parse_kernel_name(name: str):
+    """(base name, template arguments as strings) of a mangled or demangled ``mpk::`` kernel."""
+    if name.startswith("_ZN3mpk"):
+        rest = name[len("_ZN3mpk"):]
+        digits = re.match(r"\d+", rest)
+        if not digits:
+            return name, []
+        n = int(digits.group(0))
+        base = rest[len(digits.group(0)):len(digits.group(0)) + n]
+        rest = rest[len(digits.group(0)) + n:]
+        args: List[str] = []
+        if rest.startswith("I"):
+            pos = 1
+            while pos < len(rest):
+                m = _MANGLED_ARG.match(rest, pos)
+                if not m or m.group(5):
+                    break
+                args.append(m.group(1) or {"0": "false", "1": "true"}.get(m.group(2) or "", "")
+                            or ("_Float16" if m.group(3) else "float"))
+                pos = m.end()
+        return base, args
+    base = name.split("<", 1)[0].split("(", 1)[0].split("::")[-1].split()[-1]
+    if "<" not in name:
+        return base, []
+    inner = name.split("<", 1)[1].rsplit(">", 1)[0]
+    return base, [a.strip() for a in inner.split(",")]
+
+
+def base_kernel_key(name: str) -> str:
+    """Kernel role from its name; '@residual' / '@ln' are resolved by ``label_dispatches``."""
+    base, args = parse_kernel_name(name)
+    if base == "layer_tail_kernel" and len(args) >= 5:
+        if args[3] == "false":
+            return "layernorm_qkv"
+        return "layer_tail_last" if args[4] == "true" else "layer_tail"
+    if base in ("attention32_kernel", "attention_kernel"):
+        return "attention"
+    if base in ("linear_big_kernel", "linear_kernel"):
+        index = 3 if base == "linear_big_kernel" else 5
+        epi = int(args[index]) if len(args) > index and args[index].lstrip("-").isdigit() else -1
+        return {0: "qkv_proj", 1: "ffn_in", 2: "@ln", 3: "@residual", 4: "@ln"}.get(epi, "linear")
+    if base in ("ffn_ln_kernel", "ffn_wide_kernel"):
+        return "ffn_ln"
+    if base == "residual_layernorm_kernel":
+        return "layernorm"
     if "copyBuffer" in name or "copy_kernel" in name or "elementwise_kernel" in name:
         return "copy"
-    return name[:60]
+    return base[:60]
+
+
+def label_dispatches(names: List[str]) -> List[str]:
+    """Per-dispatch kernel keys in launch order.
+
+    The out-projection and the FFN-output projection can be the same kernel
+    instantiation; a residual / LayerNorm-epilogue GEMM is the out-projection
+    when the last other kernel launched was attention, and the FFN output when
+    it was the FFN-in GEMM (in the forward, and in the per-kernel timing loops,
+    which launch the kernels in forward order).
+    """
+    labels = []
+    previous = "attention"
+    for name in names:
+        key = base_kernel_key(name)
+        if key.startswith("@"):
+            prefix = "ffn_out" if previous == "ffn_in" else "out_proj"
+            key = prefix + ("_residual" if key == "@residual" else "_ln")
+        else:
+            previous = key
+        labels.append(key)
+    return labels
 
 
 def _run(config_name: str, iters: int) -> None:
@@ -324,67 +395,254 @@ def _run(config_name: str, iters: int) -> None:
     torch.cuda.synchronize()
 
 
-def _summarize(fetch_csv: str, write_csv: str, config_name: str, out: str) -> None:
+def _csv_rows(path: str):
     import csv
+    import glob
+
+    if os.path.isdir(path):
+        found = sorted(glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True)
+                       or glob.glob(os.path.join(path, "**", "*kernel_trace.csv"), recursive=True))
+        if not found:
+            raise FileNotFoundError(f"no rocprofv3 CSV under {path}")
+        path = found[0]
+    with open(path) as handle:
+        return list(csv.DictReader(handle))
+
+
+def counters_per_dispatch(path: str) -> List[Dict[str, object]]:
+    """rocprofv3 counter-collection rows -> one dict per dispatch in dispatch order:
+    {"name", "key", "ns", counter: value...}."""
+    by_id: Dict[int, Dict[str, object]] = {}
+    for row in _csv_rows(path):
+        did = int(row["Dispatch_Id"])
+        entry = by_id.setdefault(did, {"name": row["Kernel_Name"],
+                                       "ns": float(row["End_Timestamp"]) - float(row["Start_Timestamp"])})
+        entry[row["Counter_Name"]] = entry.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+    ordered = [by_id[k] for k in sorted(by_id)]
+    for entry, key in zip(ordered, label_dispatches([e["name"] for e in ordered])):
+        entry["key"] = key
+    return ordered
+
+
+def trace_per_dispatch(path: str) -> List[Dict[str, object]]:
+    """rocprofv3 kernel-trace rows -> [{"name", "key", "ns"}] in dispatch order."""
+    rows = sorted(_csv_rows(path), key=lambda r: int(r["Dispatch_Id"]))
+    out = [{"name": r["Kernel_Name"], "ns": float(r["End_Timestamp"]) - float(r["Start_Timestamp"])} for r in rows]
+    for entry, key in zip(out, label_dispatches([e["name"] for e in out])):
+        entry["key"] = key
+    return out
+
+
+def _mean_by_key(entries, field: str) -> Dict[str, float]:
+    sums: Dict[str, float] = {}
+    counts: Dict[str, int] = {}
+    for e in entries:
+        if field in e:
+            sums[e["key"]] = sums.get(e["key"], 0.0) + float(e[field])
+            counts[e["key"]] = counts.get(e["key"], 0) + 1
+    return {k: sums[k] / counts[k] for k in sums}
+
+
+def _merge_json(path: str, config_name: str, table: Dict[str, object], extra: Dict[str, object]) -> None:
     import json
-    from collections import defaultdict
 
-    def per_kernel(path: str, counter: str):
-        sums, counts, peak = defaultdict(float), defaultdict(int), defaultdict(float)
-        with open(path) as handle:
-            for row in csv.DictReader(handle):
-                if row["Counter_Name"] != counter:
-                    continue
-                key = _kernel_key(row["Kernel_Name"])
-                value = float(row["Counter_Value"])
-                sums[key] += value
-                counts[key] += 1
-                peak[key] = max(peak[key], value)
-        out = {k: sums[k] / counts[k] for k in sums}
-        if "copy" in peak:
-            out["copy"] = peak["copy"]  # the 1 GiB calibration copy is the largest copy dispatch
-        return out
-
-    fetch = per_kernel(fetch_csv, "FETCH_SIZE")
-    write = per_kernel(write_csv, "WRITE_SIZE")
-    # the calibration copy is the largest "copy" dispatch; its counters should read 1 GiB each
-    f_scale = CALIBRATION_BYTES / (fetch["copy"] * 1024.0) if fetch.get("copy") else 1.0
-    w_scale = CALIBRATION_BYTES / (write["copy"] * 1024.0) if write.get("copy") else 1.0
-    table = {"calibration": {"copy_bytes": CALIBRATION_BYTES, "fetch_scale": f_scale, "write_scale": w_scale}}
-    entry = {}
-    for key in sorted(set(fetch) | set(write)):
-        if key == "copy":
-            continue
-        fb = fetch.get(key, 0.0) * 1024.0 * f_scale
-        wb = write.get(key, 0.0) * 1024.0 * w_scale
-        entry[key] = {"fetch_bytes": fb, "write_bytes": wb, "bytes_per_launch": fb + wb}
-    table[config_name] = entry
     try:
-        with open(out) as handle:
+        with open(path) as handle:
             old = json.load(handle)
     except (OSError, ValueError):
         old = {}
-    old.update(table)
-    with open(out, "w") as handle:
+    old.update(extra)
+    old[config_name] = table
+    with open(path, "w") as handle:
         json.dump(old, handle, indent=1, sort_keys=True)
-    print(json.dumps(table, indent=1))
+
+
+def traffic_summary(fetch_path: str, write_path: str) -> Dict[str, object]:
+    """HBM bytes per launch per kernel key from FETCH_SIZE and WRITE_SIZE runs (KiB per dispatch)."""
+    fetch = counters_per_dispatch(fetch_path)
+    write = counters_per_dispatch(write_path)
+    copy_f = max((e["FETCH_SIZE"] for e in fetch if e["key"] == "copy"), default=0.0)
+    copy_w = max((e["WRITE_SIZE"] for e in write if e["key"] == "copy"), default=0.0)
+    f_scale = CALIBRATION_BYTES / (copy_f * 1024.0) if copy_f else 1.0
+    w_scale = CALIBRATION_BYTES / (copy_w * 1024.0) if copy_w else 1.0
+    fmean = _mean_by_key([e for e in fetch if e["key"] != "copy"], "FETCH_SIZE")
+    wmean = _mean_by_key([e for e in write if e["key"] != "copy"], "WRITE_SIZE")
+    table = {}
+    for key in sorted(set(fmean) | set(wmean)):
+        fb = fmean.get(key, 0.0) * 1024.0 * f_scale
+        wb = wmean.get(key, 0.0) * 1024.0 * w_scale
+        table[key] = {"fetch_bytes": fb, "write_bytes": wb, "bytes_per_launch": fb + wb}
+    calibration = {"copy_bytes": CALIBRATION_BYTES, "fetch_scale": f_scale, "write_scale": w_scale}
+    return {"kernels": table, "calibration": calibration}
+
+
+def mfma_summary(counter_path: str, trace_path: str) -> Dict[str, object]:
+    """MFMA busy fraction and counted MFMA FLOPs per kernel key.
+
+    busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs), the share of SIMD
+    cycles with the matrix core busy while the kernel ran (rocprofv3's MfmaUtil);
+    counted FLOPs = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512; rate = counted FLOPs / the
+    kernel-trace average duration (counter runs serialise and slow dispatches).
+    """
+    entries = counters_per_dispatch(counter_path)
+    durations = _mean_by_key(trace_per_dispatch(trace_path), "ns")
+    table = {}
+    for key in sorted({e["key"] for e in entries}):
+        if key == "copy":
+            continue
+        sel = [e for e in entries if e["key"] == key]
+        busy = [e["SQ_VALU_MFMA_BUSY_CYCLES"] / (e["GRBM_GUI_ACTIVE"] * SIMD_PER_GPU)
+                for e in sel if e.get("GRBM_GUI_ACTIVE")]
+        flops = [e["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512.0 for e in sel if "SQ_INSTS_VALU_MFMA_MOPS_F16" in e]
+        row = {
+            "dispatches": len(sel),
+            "mfma_busy": sum(busy) / len(busy) if busy else None,
+            "mfma_flops_per_launch": sum(flops) / len(flops) if flops else None,
+            "valu_insts_per_launch": _mean_by_key(sel, "SQ_INSTS_VALU").get(key),
+            "mfma_insts_per_launch": _mean_by_key(sel, "SQ_INSTS_MFMA").get(key),
+            "trace_avg_us": durations[key] / 1e3 if key in durations else None,
+        }
+        if row["mfma_flops_per_launch"] and row["trace_avg_us"]:
+            row["mfma_tflops"] = row["mfma_flops_per_launch"] / (row["trace_avg_us"] * 1e-6) / 1e12
+        table[key] = row
+    return table
+
+
+CONFIG_ORDER = ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5")
+
+
+def results_table(runs_dir: str, profiles_dir: str) -> str:
+    """Markdown results table: bench lines, kernel-trace averages and PMC counters."""
+    import json
+
+    def load(path):
+        try:
+            with open(path) as handle:
+                return json.load(handle)
+        except (OSError, ValueError):
+            return {}
+
+    traffic = load(os.path.join(profiles_dir, "hbm_traffic.json"))
+    mfma = load(os.path.join(profiles_dir, "mfma_counters.json"))
+    lines = [
+        "| cfg | shape (B,S,D,H,F,L) | median ms | tokens/s | fwd floor ms | fwd roofline frac | "
+        "max abs err (bench rows) | CPU strict-FP32 tokens/s (threads) | GPU/CPU |",
+        "|---|---|---|---|---|---|---|---|---|",
+    ]
+    kernel_lines = [
+        "| cfg | kernel | launches/fwd | bench avg us | rocprof avg us | bound | achieved | frac of peak | "
+        "TFLOP/s | GB/s | PMC HBM MB/launch (x algorithmic) | MFMA busy | counted MFMA TFLOP/s |",
+        "|---|---|---|---|---|---|---|---|---|---|---|---|---|",
+    ]
+    for name in CONFIG_ORDER:
+        bench = load(os.path.join(runs_dir, f"bench_{name}.json"))
+        if not bench:
+            continue
+        cfg = bench["config"]
+        shape = ",".join(str(cfg[k]) for k in ("batch", "seq_len", "d_model", "heads", "ffn_dim", "layers"))
+        cpu = bench.get("cpu_baseline") or {}
+        par = bench.get("parity") or {}
+        ratio = f"{bench['value'] / cpu['value']:.0f}x" if cpu.get("value") else "-"
+        lines.append(
+            f"| {name} | {shape} | {bench['median_ms']:.4g} | {bench['value']:.4g} | "
+            f"{bench['forward_roofline_floor_ms']:.4g} | {bench['forward_roofline_frac']:.3f} | "
+            f"{par.get('max_abs', float('nan')):.3g} ({par.get('failed', '?')}/{par.get('elements', '?')} failed) | "
+            f"{cpu.get('value', float('nan')):.4g} ({cpu.get('cores', '?')}) | {ratio} |"
+        )
+        trace_dir = os.path.join(runs_dir, f"prof_{name}")
+        try:
+            rocprof = _mean_by_key(trace_per_dispatch(trace_dir), "ns")
+        except (OSError, FileNotFoundError):
+            rocprof = {}
+        tcfg = (traffic.get(name) or {})
+        tcfg = tcfg.get("kernels", tcfg)
+        mcfg = mfma.get(name) or {}
+        for k in bench["kernels"]:
+            key = k["kernel"]
+            rp = f"{rocprof[key] / 1e3:.1f}" if key in rocprof else "-"
+            tr = tcfg.get(key)
+            alg = k.get("bytes") or k.get("algorithmic_bytes")
+            if tr:
+                ratio_t = f" ({tr['bytes_per_launch'] / alg:.2f}x)" if alg else ""
+                tr_s = f"{tr['bytes_per_launch'] / 1e6:.1f}{ratio_t}"
+            else:
+                tr_s = "-"
+            mc = mcfg.get(key) or {}
+            busy = f"{mc['mfma_busy']:.3f}" if mc.get("mfma_busy") is not None else "-"
+            ctf = f"{mc['mfma_tflops']:.0f}" if mc.get("mfma_tflops") else "-"
+            kernel_lines.append(
+                f"| {name} | {key} | {k['launches_per_forward']} | {k['avg_us']:.2f} | {rp} | {k['bound']} | "
+                f"{k['achieved']:.4g} {k['unit']} | {k['frac']:.3f} | {k['tflops']:.1f} | {k['gbps']:.0f} | "
+                f"{tr_s} | {busy} | {ctf} |"
+            )
+    return "\n".join(lines) + "\n\n" + "\n".join(kernel_lines) + "\n"
+
+
+def parity_table(records_path: str) -> str:
+    import json
+
+    with open(records_path) as handle:
+        records = json.load(handle)
+    order = {n: i for i, n in enumerate(CONFIG_ORDER)}
+    records.sort(key=lambda r: (order.get(r["config"], 99), r["trial"]))
+    lines = [
+        "| cfg | trial | input seed | elements compared | failed | max abs err | max rel err | mean abs err | "
+        "GPU vs CPU oracle (one row) |",
+        "|---|---|---|---|---|---|---|---|---|",
+    ]
+    for r in records:
+        cross = r.get("gpu_vs_cpu_oracle_max_abs")
+        lines.append(
+            f"| {r['config']} | {r['trial']} | {r['input_seed']} | {r['elements']:,} | {r['failed']} | "
+            f"{r['max_abs']:.6g} | {r['max_rel']:.6g} | {r['mean_abs']:.3g} | "
+            f"{'-' if cross is None else f'{cross:.2g}'} |"
+        )
+    return "\n".join(lines) + "\n"
+
+
+def _main(argv=None) -> None:
+    import argparse
+
+    parser = argparse.ArgumentParser(prog="python -m tiktoktechjam2026_amd.profiling")
+    sub = parser.add_subparsers(dest="cmd", required=True)
+    p_run = sub.add_parser("run")
+    p_run.add_argument("--config", default="cfg5")
+    p_run.add_argument("--iters", type=int, default=3)
+    p_tr = sub.add_parser("traffic")
+    p_tr.add_argument("fetch")
+    p_tr.add_argument("write")
+    p_tr.add_argument("--config", required=True)
+    p_tr.add_argument("--out", default="profiles/hbm_traffic.json")
+    p_mf = sub.add_parser("mfma")
+    p_mf.add_argument("counters")
+    p_mf.add_argument("trace")
+    p_mf.add_argument("--config", required=True)
+    p_mf.add_argument("--out", default="profiles/mfma_counters.json")
+    p_tab = sub.add_parser("table")
+    p_tab.add_argument("runs_dir")
+    p_tab.add_argument("--profiles", default="profiles")
+    p_tab.add_argument("--out", default=None)
+    p_par = sub.add_parser("parity-table")
+    p_par.add_argument("records")
+    p_par.add_argument("--out", default=None)
+    args = parser.parse_args(argv)
+    if args.cmd == "run":
+        _run(args.config, args.iters)
+    elif args.cmd == "traffic":
+        summary = traffic_summary(args.fetch, args.write)
+        _merge_json(args.out, args.config, summary["kernels"], {"calibration": summary["calibration"]})
+        print(summary)
+    elif args.cmd == "mfma":
+        table = mfma_summary(args.counters, args.trace)
+        _merge_json(args.out, args.config, table, {"simd_per_gpu": SIMD_PER_GPU})
+        print(table)
+    else:
+        text = results_table(args.runs_dir, args.profiles) if args.cmd == "table" else parity_table(args.records)
+        if args.out:
+            with open(args.out, "w") as handle:
+                handle.write(text)
+        print(text, end="")
 
 
 if __name__ == "__main__":
-    import argparse
-
-    parser = argparse.ArgumentParser()
-    sub = parser.add_subparsers(dest="cmd", required=True)
-    p_run = sub.add_parser("run")
-    p_run.add_argument("--config", default="cfg2")
-    p_run.add_argument("--iters", type=int, default=3)
-    p_sum = sub.add_parser("summarize")
-    p_sum.add_argument("fetch_csv")
-    p_sum.add_argument("write_csv")
-    p_sum.add_argument("--config", default="cfg2")
-    p_sum.add_argument("--out", default="profiles/hbm_traffic.json")
-    args = parser.parse_args()
-    if args.cmd == "run":
-        _run(args.config, args.iters)
-    else:
-        _summarize(args.fetch_csv, args.write_csv, args.config, args.out)
+    _main()
