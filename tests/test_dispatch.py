@@ -16,7 +16,8 @@ def test_benchmark_config_routes():
     for cfg in BENCHMARK_CONFIGS.values():
         route = dispatch.plan(cfg)
         narrow = cfg.d_model < dispatch.WIDE_GEMM_FROM
-        assert route.supported and route.fuse_attention_output_norm == narrow and route.fuse_full_ffn == narrow
+        assert route.supported and route.fuse_attention_output_norm == narrow
+        assert route.fuse_full_ffn == (narrow or cfg.d_model == dispatch.WIDE_FFN_WIDTH)
         assert route.normalized_dtype == torch.float16
 
 
@@ -32,8 +33,13 @@ def test_wide_layernorm_epilogue_route():
 
     costs = profiling.forward_costs(cfg5, 2, dispatch.plan(cfg5))
     assert costs["layernorm"].launches_per_forward == 1
-    assert {"out_proj_ln", "ffn_in", "ffn_out_ln"} <= set(costs)
-    assert "ffn_out_residual" not in costs and "out_proj_residual" not in costs
+    assert {"out_proj_ln", "ffn_ln"} <= set(costs)
+    assert not {"ffn_in", "ffn_out_ln", "ffn_out_residual", "out_proj_residual"} & set(costs)
+    # without the FFN fusion the FFN runs as two GEMMs, the second with the LayerNorm epilogue
+    unfused = dispatch.plan(cfg5, enable_full_ffn_fusion=False)
+    assert not unfused.fuse_full_ffn and not unfused.wide_ln_epilogue
+    # widths above the wide FFN kernel's hidden limit keep the GEMM route
+    assert not dispatch.plan(TransformerConfig(2, 8, 256, 8, dispatch.WIDE_FFN_MAX_F + 32, 1, True)).fuse_full_ffn
 
 
 def test_enable_flags_change_the_route():
@@ -64,6 +70,11 @@ def test_python_tables_match_library(built_library):
         assert bool(lib.mpk_layernorm_qkv_supported(d)) == (d in dispatch.LAYERNORM_QKV_WIDTHS)
         for f in (32, 64, 96, 128, 256, 512, 1024, 2048):
             assert bool(lib.mpk_layer_tail_supported(d, f)) == ((d, f) in dispatch.LAYER_TAIL_SHAPES)
+    # the wide fused FFN (variant 3) is the library's choice exactly where the route fuses it
+    for d in (128, 256, 512):
+        for f in (32, 96, 1024, dispatch.WIDE_FFN_MAX_F, dispatch.WIDE_FFN_MAX_F + 32):
+            wide = d == dispatch.WIDE_FFN_WIDTH and f <= dispatch.WIDE_FFN_MAX_F
+            assert (lib.mpk_ffn_residual_layernorm_auto_variant(65536, d, f) == 3) == wide, (d, f)
 
 
 def test_model_interface_mirrors_reference():

@@ -286,8 +286,26 @@ def test_linear_residual_layer_norm_wide_rejects(hip_device):
 @pytest.mark.parametrize("m", [9, 3000])
 @pytest.mark.parametrize("variant", [1, 2])
 def test_ffn_residual_layernorm(hip_device, d, f, m, variant):
+    _check_ffn(hip_device, d, f, m, variant, torch.float16)
+
+
+# The wide kernel (variant 3, d_model 256): one chunk (f 32), no steady chunk (f 64), odd chunk
+# counts, the cfg5 shape; row counts below one tile, ragged, and with two or more tiles per
+# workgroup of the persistent grid (256 workgroups x 128 rows per pass) and a ragged last tile.
+@pytest.mark.parametrize("f", [32, 64, 96, 1024])
+@pytest.mark.parametrize("m", [9, 3000, 2 * 256 * 128 + 37])
+def test_ffn_wide_residual_layernorm(hip_device, f, m):
+    _check_ffn(hip_device, 256, f, m, 3, torch.float16)
+
+
+def test_ffn_wide_fp32_input(hip_device):
+    _check_ffn(hip_device, 256, 1024, 777, 3, torch.float32)
+
+
+def _check_ffn(hip_device, d, f, m, variant, x_dtype):
     from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_ffn_add_layer_norm
 
+    print(f"\n[ffn] d={d} f={f} m={m} variant={variant} x={x_dtype}", flush=True)
     lin_in = _linear(d, f, hip_device, 31)
     lin_out = _linear(f, d, hip_device, 32)
     norm = _norm(d, hip_device, 33)
@@ -295,7 +313,7 @@ def test_ffn_residual_layernorm(hip_device, d, f, m, variant):
     resid = _randn((m, d), 35, 2.0)
     for out_dtype in (torch.float16, torch.float32):
         r_out, n_out = mixed_ffn_add_layer_norm(
-            x.to(hip_device, torch.float16), lin_in, lin_out, resid.to(hip_device), norm,
+            x.to(hip_device, x_dtype), lin_in, lin_out, resid.to(hip_device), norm,
             normalized_dtype=out_dtype, variant=variant,
         )
         h = _ref_linear(x, lin_in, True)          # FP32 GELU on the accumulator ...

@@ -46,6 +46,10 @@ COMMON_FLAGS = [
 # inputs (masked scores are -inf, exp2(-inf) = 0), so its max reductions need
 # no NaN canonicalisation.
 EXTRA_FLAGS = {"attention.hip": ["-fno-honor-nans"]}
+# Sources whose kernels keep MFMA accumulators in AGPRs: the wide fused FFN runs one
+# wave per SIMD with 32 x D FP32 accumulators, more than the 256 arch VGPRs hold
+# beside its operands.
+AGPR_ACCUMULATORS = {"ffn_wide.hip"}
 
 
 def _hipcc() -> str:
@@ -61,7 +65,12 @@ def sources() -> List[str]:
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [_hipcc(), *COMMON_FLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
+    name = os.path.basename(src)
+    flags = list(COMMON_FLAGS)
+    if name in AGPR_ACCUMULATORS:
+        i = flags.index("-amdgpu-mfma-vgpr-form")
+        del flags[i - 1:i + 1]
+    cmd = [_hipcc(), *flags, *EXTRA_FLAGS.get(name, []), "-c", src, "-o", obj]
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {os.path.basename(src)}:\n{proc.stdout}")

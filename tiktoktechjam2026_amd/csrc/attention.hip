@@ -460,15 +460,11 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 // VALU work of the same wave run beside it (the 16x16x32 form leaves little
 // room for that, and at these head dims the softmax is the larger cost).
 //
-// 32x32x16 operand layouts (lane l, i = l % 32, h = l / 32):
-//   A (32 x 16): row i, k = 8h .. 8h+7     B (16 x 32): column i, k = 8h .. 8h+7
-//   C (32 x 32): column i, rows 8J + 4h + I in register 4J + I  (J, I = 0..3)
-// MFMA row rho of a 32-row block is fed from row kappa(rho) of the tile
-// (keys for S^T, head dims for O^T):
-//   kappa(8J + 4h + I) = 16 (J >> 1) + 8h + 4 (J & 1) + I,
-// so the lane (i, h) accumulator register e = 8s + j (s = 0, 1; j = 0..7) holds
-// tile row 16s + 8h + j.  For S^T that is the B operand of the two 16-key steps
-// of the P V product; for O^T it is 2 x 8 consecutive head dims of query i.
+// 32x32x16 operand layouts and the kappa32 row map are described in mpk_common.h:
+// MFMA row rho of a 32-row block is fed from row kappa32(rho) of the tile (keys
+// for S^T, head dims for O^T), so the lane (i, h) accumulator register e = 8s + j
+// holds tile row 16s + 8h + j.  For S^T that is the B operand of the two 16-key
+// steps of the P V product; for O^T it is 2 x 8 consecutive head dims of query i.
 // Each lane owns one query (i) and half of its keys, so a row max is a
 // lane-local max plus one permlane32 swap.
 //
@@ -483,17 +479,6 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 // it the binding unit at these head dims.  Row sums of fp16(P) come from a 16x16x32 product with a 0/1
 // A operand (rows 0 and 1 pick the queries i and i + 16 out of the P fragment
 // layout), so l sums exactly the FP16 weights that multiply V.
-typedef float f16v __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ f16v mfma32x32(const h8& a, const h8& b, const f16v& c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ int kappa32(int rho) {
-  const int J = rho >> 3, hh = (rho >> 2) & 1, I = rho & 3;
-  return 16 * (J >> 1) + 8 * hh + 4 * (J & 1) + I;
-}
-
 template <int HD, int NW, int KTILE, typename IT, typename OT, bool KEYMASK>
 __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
   constexpr int NT = 64 * NW;

@@ -17,25 +17,12 @@
 // W_in / W_out are staged through LDS in chunks of FC hidden features; when the
 // whole F fits (one chunk) the workgroup loads them once and then walks a
 // persistent loop over row tiles without further barriers.
-#include "mpk_common.h"
+#include <algorithm>
+#include <type_traits>
+
+#include "ffn.h"
 
 namespace mpk {
-
-struct FfnArgs {
-  const void* x;
-  const _Float16* w_in;   // [F, D]
-  const _Float16* b_in;   // [F]
-  const _Float16* w_out;  // [D, F]
-  const _Float16* b_out;  // [D]
-  const float* residual;  // [M, D]
-  const float* gamma;
-  const float* beta;
-  float* residual_out;
-  void* normalized_out;
-  int64_t m;
-  int f;
-  float eps;
-};
 
 template <int D, int FC, int TM, typename XT, typename OT>
 __global__ __launch_bounds__(kBlock) void ffn_ln_kernel(FfnArgs a) {
@@ -234,6 +221,9 @@ static hipError_t launch_ffn(const FfnArgs& a, hipStream_t s) {
 
 template <typename XT, typename OT>
 static hipError_t ffn_dispatch(int variant, const FfnArgs& a, int d, hipStream_t s) {
+  // variant 3: the wide kernel (d_model 256, 32x32x16 MFMAs, 128-token workgroups)
+  if (variant == 3) return launch_ffn_wide(a, d, kF16, std::is_same<XT, float>::value ? kF32 : kF16,
+                                           std::is_same<OT, float>::value ? kF32 : kF16, s);
   // variant 1: TM=1; variant 2: TM=2 (D <= 256)
   const bool two = variant == 2;
   switch (d) {
@@ -253,7 +243,7 @@ using namespace mpk;
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 extern "C" int mpk_ffn_residual_layernorm_auto_variant(int64_t m, int32_t d, int32_t f) {
-  (void)f;
+  if (ffn_wide_supported(d, f)) return 3;
   if (d <= 128 && m >= 64 * 1024) return 2;
   return 1;
 }
@@ -276,7 +266,7 @@ extern "C" int mpk_ffn_residual_layernorm(const void* x, int x_dtype, const void
     return MPK_EALIGN;
   if (m == 0) return MPK_OK;
   if (variant == 0) variant = mpk_ffn_residual_layernorm_auto_variant(m, d, f);
-  if (variant != 1 && variant != 2) return MPK_EUNSUPPORTED;
+  if (variant < 1 || variant > 3) return MPK_EUNSUPPORTED;
   FfnArgs a{};
   a.x = x; a.w_in = static_cast<const _Float16*>(w_in); a.b_in = static_cast<const _Float16*>(b_in);
   a.w_out = static_cast<const _Float16*>(w_out); a.b_out = static_cast<const _Float16*>(b_out);

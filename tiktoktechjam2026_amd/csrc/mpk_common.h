@@ -50,6 +50,33 @@ __device__ __forceinline__ f4 mfma16(const h4& a, const h4& b, const f4& c) {
 
 __device__ __forceinline__ int pair_row(int q, int t) { return 8 * (q >> 2) + 4 * t + (q & 3); }
 
+// ---- 32x32x16 products ----
+// Operand layouts of v_mfma_f32_32x32x16_f16 (lane l, i = l % 32, h = l / 32):
+//   A (32 x 16): row i, k = 8h .. 8h+7     B (16 x 32): column i, k = 8h .. 8h+7
+//   C (32 x 32): column i, rows 8J + 4h + I in register 4J + I  (J, I = 0..3)
+// A kernel that feeds MFMA row rho of a 32-row block from row kappa32(rho) of its
+// operand,
+//   kappa32(8J + 4h + I) = 16 (J >> 1) + 8h + 4 (J & 1) + I,
+// finds in accumulator register e = 8s + j (s = 0, 1; j = 0..7) of lane (i, h) the
+// operand row 16s + 8h + j: two runs of 8 consecutive rows per lane, which is the
+// B operand of the two 16-deep k-steps of a following product over those rows.
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f16v mfma32x32(const h8& a, const h8& b, const f16v& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int kappa32(int rho) {
+  const int J = rho >> 3, hh = (rho >> 2) & 1, I = rho & 3;
+  return 16 * (J >> 1) + 8 * hh + 4 * (J & 1) + I;
+}
+
+// Sum of v over lanes l and l ^ 32 (the two halves of a 32x32 C column), bit-identical in both.
+__device__ __forceinline__ float sum_over_halves(float v) {
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Index of the calling wave in its workgroup, as a wave-uniform (scalar) value:
 // branches on quantities derived from it compile to scalar branches instead of
 // exec-mask divergence, and its address arithmetic stays on the scalar unit.

@@ -25,6 +25,12 @@ a 256 x 256 output tile holds whole rows, so the row statistics are exchanged
 across its waves in LDS and no separate LayerNorm launch re-reads the residual
 stream.
 
+At d_model 256 the FFN runs as one kernel too (``WIDE_FFN_WIDTH``,
+``fuse_full_ffn``): both products on 32x32 MFMAs with the hidden activation in
+registers, the residual add and the next LayerNorm in its epilogue, so that
+route launches, per layer, the QKV projection, attention, the out-projection
+(+ residual + LayerNorm) and the FFN (+ residual + LayerNorm).
+
 When the whole layer tail fits one kernel (``LAYER_TAIL_SHAPES``) the forward
 runs 1 + 2L launches: LayerNorm+QKV, then per layer attention and the fused
 tail (out-proj+LN2+FFN+LN1'+QKV', or the final LayerNorm on the last layer).
@@ -35,6 +41,7 @@ Tile variants (see the kernel sources for the exact tiles):
   out-proj + LN            1: 64 rows/WG           2: 128 rows/WG (d <= 128)
                            3: 256x256 GEMM tiles, cross-wave LayerNorm (d = 256)
   fused FFN + LN           1: 16 rows/wave         2: 32 rows/wave (d <= 256)
+                           3: 32x32-MFMA wide kernel, 128-row workgroups (d = 256)
   attention                1: 16 queries/wave      2: 32 queries/wave (hd <= 64)
                            3-5: 128-key tiles / 8-wave workgroups
                            6-8: 32x32-MFMA kernel (hd 32 and 64)
@@ -58,6 +65,10 @@ LAYERNORM_QKV_WIDTHS = frozenset({32, 64, 128})
 WIDE_GEMM_FROM = 256
 # GEMM-route width whose residual projections fuse the next LayerNorm (256 x 256 tiles).
 WIDE_LN_EPILOGUE_WIDTH = 256
+# Width of the wide fused FFN kernel (32x32-MFMA, hidden on chip) and its largest ffn_dim;
+# must equal ffn_wide_supported in the library.
+WIDE_FFN_WIDTH = 256
+WIDE_FFN_MAX_F = 8192
 
 
 @dataclass(frozen=True)
@@ -130,7 +141,8 @@ def plan(
         return Route(False, "d_model above 2048")
     narrow = d in LN_FUSED_WIDTHS and d < WIDE_GEMM_FROM
     fuse_out = enable_attention_output_norm_fusion and narrow
-    fuse_ffn = enable_full_ffn_fusion and narrow and f % 32 == 0
+    wide_ffn = d == WIDE_FFN_WIDTH and f <= WIDE_FFN_MAX_F
+    fuse_ffn = enable_full_ffn_fusion and (narrow or wide_ffn) and f % 32 == 0
     # The layer-tail kernel chains out-proj+LN2 -> FFN+LN -> next QKV; it needs both
     # fusions, the FP16 normalized stream and FP16 attention I/O.
     fuse_tail = (

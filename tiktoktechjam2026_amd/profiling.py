@@ -316,7 +316,8 @@ def parse_kernel_name(name: str):
                             or ("_Float16" if m.group(3) else "float"))
                 pos = m.end()
         return base, args
-    base = name.split("<", 1)[0].split("(", 1)[0].split("::")[-1].split()[-1]
+    words = name.split("<", 1)[0].split("(", 1)[0].split("::")[-1].split()
+    base = words[-1] if words else name
     if "<" not in name:
         return base, []
     inner = name.split("<", 1)[1].rsplit(">", 1)[0]
