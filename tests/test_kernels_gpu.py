@@ -412,6 +412,8 @@ def test_attention_32x32_noncausal_fp32io_keymask_negative_scale(hip_device, var
         out = attention(q, k, v, scale, causal=False, variant=variant)
         assert out.dtype == torch.float32
         _close(out, _ref_attention(q, k, v, scale, False), 3e-3, 3e-3, "non-causal fp32 io (32x32)")
+        out_h = attention(q.half(), k.half(), v.half(), scale, causal=False, variant=variant)
+        _close(out_h, _ref_attention(q, k, v, scale, False), 3e-3, 3e-3, "non-causal fp16 io (32x32)")
         out_n = attention(q.half(), k.half(), v.half(), -scale, causal=True, variant=variant)
         _close(out_n, _ref_attention(q, k, v, -scale, True), 3e-3, 3e-3, "negative scale (32x32)")
         lengths = torch.tensor([max(1, s - 37 * (i + 1)) for i in range(b)])
