@@ -71,7 +71,8 @@ def test_traffic_summary_scales_by_the_calibration_copy(tmp_path):
 def test_mfma_summary_busy_fraction_and_rate(tmp_path):
     counters = tmp_path / "mfma.csv"
     trace = tmp_path / "trace.csv"
-    _write_counters(counters, [(ATTN, {"SQ_VALU_MFMA_BUSY_CYCLES": 512.0 * 1000, "GRBM_GUI_ACTIVE": 1000.0,
+    # GRBM_GUI_ACTIVE arrives summed over the 8 XCDs: 8000 = 1000 cycles of kernel time
+    _write_counters(counters, [(ATTN, {"SQ_VALU_MFMA_BUSY_CYCLES": 512.0 * 1000, "GRBM_GUI_ACTIVE": 8000.0,
                                        "SQ_INSTS_VALU_MFMA_MOPS_F16": 1e6}, 5000)])
     with open(trace, "w", newline="") as handle:
         writer = csv.DictWriter(handle, fieldnames=["Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp"])

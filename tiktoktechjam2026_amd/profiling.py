@@ -291,6 +291,10 @@ def describe_rate(value: float) -> str:
 
 CALIBRATION_BYTES = 1 << 30
 SIMD_PER_GPU = 1024  # MI355X: 256 CUs x 4 SIMDs (rocprofv3 agent info Simd_Count)
+# rocprofv3 reports GRBM_GUI_ACTIVE summed over the 8 XCDs of the MI355X (each XCD
+# counts the kernel's busy cycles on its own clock domain), so one kernel-duration
+# worth of cycles is GRBM_GUI_ACTIVE / 8.
+XCD_PER_GPU = 8
 
 _MANGLED_ARG = re.compile(r"Li(-?\d+)E|Lb([01])E|(DF16_)|(f)|(E)")
 
@@ -480,8 +484,8 @@ def traffic_summary(fetch_path: str, write_path: str) -> Dict[str, object]:
 def mfma_summary(counter_path: str, trace_path: str) -> Dict[str, object]:
     """MFMA busy fraction and counted MFMA FLOPs per kernel key.
 
-    busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs), the share of SIMD
-    cycles with the matrix core busy while the kernel ran (rocprofv3's MfmaUtil);
+    busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs x SIMDs), the share of
+    SIMD cycles with the matrix core busy while the kernel ran;
     counted FLOPs = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512; rate = counted FLOPs / the
     kernel-trace average duration (counter runs serialise and slow dispatches).
     """
@@ -492,7 +496,7 @@ def mfma_summary(counter_path: str, trace_path: str) -> Dict[str, object]:
         if key == "copy":
             continue
         sel = [e for e in entries if e["key"] == key]
-        busy = [e["SQ_VALU_MFMA_BUSY_CYCLES"] / (e["GRBM_GUI_ACTIVE"] * SIMD_PER_GPU)
+        busy = [e["SQ_VALU_MFMA_BUSY_CYCLES"] * XCD_PER_GPU / (e["GRBM_GUI_ACTIVE"] * SIMD_PER_GPU)
                 for e in sel if e.get("GRBM_GUI_ACTIVE")]
         flops = [e["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512.0 for e in sel if "SQ_INSTS_VALU_MFMA_MOPS_F16" in e]
         row = {
@@ -579,6 +583,100 @@ def results_table(runs_dir: str, profiles_dir: str) -> str:
     return "\n".join(lines) + "\n\n" + "\n".join(kernel_lines) + "\n"
 
 
+RESULTS_HEADER = """# Forward results on one MI355X: all five benchmark configurations
+
+Regenerate this page (repository root; the GPU-box commands write `gpurun_out/`):
+
+```
+# on the GPU box, per configuration N = 1..5
+python bench.py --config cfgN --json-out gpurun_out/bench_cfgN.json
+cd /tmp && export TMPDIR=/tmp && rocprofv3 --kernel-trace --stats --output-format csv \\
+    -d $GRAFT_REPO_ROOT/gpurun_out/prof_cfgN -o run -- \\
+    python3 $GRAFT_REPO_ROOT/bench.py --config cfgN --no-cpu-baseline --steps 20 --warmup 3
+# on the GPU box, counter passes for N = 2, 4, 5 (one rocprofv3 run per pass; eager forward of
+# one microbatch, 3 iterations, after a 1 GiB copy that calibrates FETCH_SIZE / WRITE_SIZE)
+cd /tmp && export TMPDIR=/tmp && PYTHONPATH=$GRAFT_REPO_ROOT rocprofv3 --pmc FETCH_SIZE --output-format csv \\
+    -d $GRAFT_REPO_ROOT/gpurun_out/pmc_cfgN_FETCH_SIZE -o run -- python3 -m tiktoktechjam2026_amd.profiling run --config cfgN
+(same with --pmc WRITE_SIZE -> pmc_cfgN_WRITE_SIZE)
+(same with --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU SQ_INSTS_MFMA SQ_WAVES \\
+    GRBM_GUI_ACTIVE -> pmc_cfgN_SQ_VALU_MFMA_BUSY_CYCLES)
+(same with --kernel-trace instead of --pmc ... -> trace_run_cfgN: the durations the MFMA rates use)
+# then, on any host
+python -m tiktoktechjam2026_amd.profiling traffic gpurun_out/pmc_cfgN_FETCH_SIZE gpurun_out/pmc_cfgN_WRITE_SIZE --config cfgN
+python -m tiktoktechjam2026_amd.profiling mfma gpurun_out/pmc_cfgN_SQ_VALU_MFMA_BUSY_CYCLES gpurun_out/trace_run_cfgN --config cfgN
+python -m tiktoktechjam2026_amd.profiling table gpurun_out --out profiles/forward_all_configs_mi355x.md
+```
+
+- median ms: HIP-event median per forward (HIP-graph replay for cfg1-4; cfg5 runs eagerly as
+  8 microbatches of 64 into a preallocated output, and its figures cover all 512 sequences).
+- fwd floor: the forward's roofline time, the sum over kernels of max(FLOPs / 2.5 PFLOP/s,
+  algorithmic bytes / 8 TB/s); fwd roofline frac = floor / measured ms per step.
+- errors: GPU output against the strict-FP32 oracle under |err| <= 0.002 or <= 0.02 |ref| on the
+  batch rows the CPU baseline computes; every element of every configuration is compared in
+  `parity_all_configs_mi355x.md`.
+- CPU: the strict-FP32 oracle on the box's host CPU (threads = the process's CPU affinity), a
+  bounded sample of whole sequences of the same input.
+- PMC HBM bytes: FETCH_SIZE + WRITE_SIZE per dispatch (KiB), scaled by what the same counters read
+  for the 1 GiB copy kernel (`calibration` in `hbm_traffic.json`), against the algorithmic bytes.
+- MFMA busy: SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs); counted MFMA
+  TFLOP/s: SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 FLOPs / the kernel-trace duration (the kernels also
+  run MFMAs that the algorithmic count does not include, such as attention's row sums and the
+  full blocks on the causal diagonal).
+
+"""
+
+
+def results_page(runs_dir: str, profiles_dir: str) -> str:
+    return RESULTS_HEADER + results_table(runs_dir, profiles_dir)
+
+
+def trace_page(prof_dir: str, config_name: str) -> str:
+    """Markdown summary of a rocprofv3 ``--kernel-trace --stats`` run of bench.py."""
+    import csv
+    import glob
+
+    found = sorted(glob.glob(os.path.join(prof_dir, "**", "*kernel_stats.csv"), recursive=True))
+    if not found:
+        raise FileNotFoundError(f"no kernel_stats.csv under {prof_dir}")
+    with open(found[0]) as handle:
+        rows = list(csv.DictReader(handle))
+    from .config import BENCHMARK_CONFIGS
+
+    c = BENCHMARK_CONFIGS[config_name]
+    lines = [
+        f"# rocprofv3 kernel trace: {config_name} forward (B{c.batch_size} S{c.seq_len} D{c.d_model} "
+        f"H{c.num_heads} F{c.ffn_dim} L{c.num_layers})",
+        "",
+        "Command (repository root on the GPU box), then the summary on any host:",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp && rocprofv3 --kernel-trace --stats --output-format csv \\",
+        f"    -d $GRAFT_REPO_ROOT/gpurun_out/prof_{config_name} -o run -- \\",
+        f"    python3 $GRAFT_REPO_ROOT/bench.py --config {config_name} --no-cpu-baseline --steps 20 --warmup 3",
+        f"python -m tiktoktechjam2026_amd.profiling trace-page gpurun_out/prof_{config_name} --config {config_name} "
+        f"--out profiles/{config_name}_forward_kernel_trace.md",
+        "```",
+        "",
+        "The run covers bench.py's warm-up and timed forwards plus its per-kernel timing loops, so",
+        "call counts exceed the launches of one forward.",
+        "",
+        "| kernel | role | calls | avg us | min us | max us | share of GPU time |",
+        "|---|---|---|---|---|---|---|",
+    ]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        name = r["Name"]
+        base, args = parse_kernel_name(name)
+        role = base_kernel_key(name)
+        role = {"@residual": "residual GEMM", "@ln": "LayerNorm-epilogue GEMM"}.get(role, role)
+        own = name.startswith("_ZN3mpk") or "mpk::" in name
+        label = f"`{base}<{', '.join(args)}>`" if args and own else f"`{base}`"
+        lines.append(
+            f"| {label} | {role} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+            f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f} % |"
+        )
+    return "\n".join(lines) + "\n"
+
+
 def parity_table(records_path: str) -> str:
     import json
 
@@ -623,6 +721,10 @@ def _main(argv=None) -> None:
     p_tab.add_argument("runs_dir")
     p_tab.add_argument("--profiles", default="profiles")
     p_tab.add_argument("--out", default=None)
+    p_tp = sub.add_parser("trace-page")
+    p_tp.add_argument("prof_dir")
+    p_tp.add_argument("--config", required=True)
+    p_tp.add_argument("--out", default=None)
     p_par = sub.add_parser("parity-table")
     p_par.add_argument("records")
     p_par.add_argument("--out", default=None)
@@ -635,10 +737,15 @@ def _main(argv=None) -> None:
         print(summary)
     elif args.cmd == "mfma":
         table = mfma_summary(args.counters, args.trace)
-        _merge_json(args.out, args.config, table, {"simd_per_gpu": SIMD_PER_GPU})
+        _merge_json(args.out, args.config, table, {"simd_per_gpu": SIMD_PER_GPU, "xcd_per_gpu": XCD_PER_GPU})
         print(table)
     else:
-        text = results_table(args.runs_dir, args.profiles) if args.cmd == "table" else parity_table(args.records)
+        if args.cmd == "table":
+            text = results_page(args.runs_dir, args.profiles)
+        elif args.cmd == "trace-page":
+            text = trace_page(args.prof_dir, args.config)
+        else:
+            text = parity_table(args.records)
         if args.out:
             with open(args.out, "w") as handle:
                 handle.write(text)
