@@ -86,13 +86,14 @@ int mpk_linear_residual_layernorm(const void* x, int x_dtype, const void* w, con
 int mpk_linear_residual_layernorm_auto_variant(int64_t m, int32_t d);
 
 /*
- * Projection with a different input width + residual + LayerNorm, on 256 x 256
- * GEMM tiles whose LayerNorm statistics are exchanged across waves in LDS:
+ * Projection with any input width + residual + LayerNorm, on GEMM tiles that hold
+ * whole rows (256 x 256 for n == 256, 128 x 512 for n == 512) and whose LayerNorm
+ * statistics are exchanged across waves in LDS:
  *   residual_out = fp16(x) * w^T + b + residual            (FP32)
  *   normalized_out = LayerNorm(residual_out) * gamma + beta
  * x: [m, k] in x_dtype; w: [n, k] FP16; b: [n] FP16; residual, residual_out:
  * [m, n] FP32 (residual_out may alias residual); gamma, beta: [n] FP32.
- * n == 256, k % 8 == 0.
+ * n in {256, 512}, k % 8 == 0.
  * Replaces, for the wide route, the reference's FFN-output projection plus its
  * residual add and the next LayerNorm (generic FFN mixed_precision/transformer.py:664-672
  * followed by mixed_add_layer_norm / fused_add_layer_norm at :674-690); with k == n it

@@ -22,15 +22,23 @@ def test_benchmark_config_routes():
 
 
 def test_wide_layernorm_epilogue_route():
-    """d_model 256 (cfg5): the residual GEMMs carry the next LayerNorm; other widths and
-    disabled fusions keep the separate LayerNorm launches."""
+    """d_model 256 (cfg5) and 512 (cfg4): the residual GEMMs carry the next LayerNorm; other
+    widths and disabled fusions keep the separate LayerNorm launches."""
     flags = {name: dispatch.plan(cfg).wide_ln_epilogue for name, cfg in BENCHMARK_CONFIGS.items()}
-    assert flags == {"cfg1": False, "cfg2": False, "cfg3": False, "cfg4": False, "cfg5": True}
+    assert flags == {"cfg1": False, "cfg2": False, "cfg3": False, "cfg4": True, "cfg5": True}
+    from tiktoktechjam2026_amd import profiling
+
+    cfg4 = BENCHMARK_CONFIGS["cfg4"]
+    costs4 = profiling.forward_costs(cfg4, 2, dispatch.plan(cfg4))
+    # d 512: the out-projection carries LN2; the FFN output keeps its LayerNorm (1 + L launches)
+    assert dispatch.plan(cfg4).wide_ln_ffn_out is False and dispatch.plan(BENCHMARK_CONFIGS["cfg5"]).wide_ln_ffn_out
+    assert costs4["layernorm"].launches_per_forward == 1 + cfg4.num_layers
+    assert {"out_proj_ln", "ffn_in", "ffn_out_residual"} <= set(costs4)
+    assert not {"out_proj_residual", "ffn_out_ln"} & set(costs4)
+    assert not dispatch.plan(TransformerConfig(2, 8, 384, 8, 64, 1, True)).wide_ln_epilogue
     cfg5 = BENCHMARK_CONFIGS["cfg5"]
     assert not dispatch.plan(cfg5, enable_attention_output_norm_fusion=False).wide_ln_epilogue
     assert not dispatch.plan(cfg5, enable_full_ffn_fusion=False).wide_ln_epilogue
-    from tiktoktechjam2026_amd import profiling
-
     costs = profiling.forward_costs(cfg5, 2, dispatch.plan(cfg5))
     assert costs["layernorm"].launches_per_forward == 1
     assert {"out_proj_ln", "ffn_ln"} <= set(costs)

@@ -228,16 +228,18 @@ def test_linear_residual_layernorm(hip_device, d, m, variant):
             _close(n_out, _ln64(r64, norm), tol, tol, "normalized_out")
 
 
-@pytest.mark.parametrize("k", [256, 1024, 136])
-@pytest.mark.parametrize("m", [7, 300, 5000])
-def test_linear_residual_layer_norm_wide(hip_device, k, m):
-    """256 x 256 GEMM tiles with the cross-wave LayerNorm epilogue (n = 256, any k % 8 == 0):
-    ragged rows (m not a multiple of the 256-row tile), K not a multiple of the 64-wide chunk,
-    FP16/FP32 inputs and outputs, and the in-place form (residual_out aliasing residual)."""
+@pytest.mark.parametrize("n,k", [(256, 256), (256, 1024), (256, 136), (512, 512), (512, 2048), (512, 40)])
+@pytest.mark.parametrize("m", [7, 300, 5000, 256 * 128 + 77])
+def test_linear_residual_layer_norm_wide(hip_device, n, k, m):
+    """GEMM tiles holding whole rows with the cross-wave LayerNorm epilogue (n = 256 on
+    256 x 256 tiles, n = 512 on 128 x 512 tiles with 32-wide K chunks; any k % 8 == 0):
+    ragged rows (m not a multiple of the row tile, and more tiles than workgroups of the
+    persistent grid), K not a multiple of the chunk, FP16/FP32 inputs and outputs, and the
+    in-place form (residual_out aliasing residual)."""
     from tiktoktechjam2026_amd import _lib
     from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear_residual_layer_norm
 
-    n = 256
+    print(f"\n[wide ln] n={n} k={k} m={m}", flush=True)
     lin = _linear(k, n, hip_device, 25)
     norm = _norm(n, hip_device, 26)
     x = _randn((m, k), 27)
@@ -272,7 +274,7 @@ def test_linear_residual_layer_norm_wide_rejects(hip_device):
     from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear_residual_layer_norm
 
     norm = _norm(128, hip_device, 1)
-    lin = _linear(256, 128, hip_device, 2)  # out_features != 256
+    lin = _linear(256, 128, hip_device, 2)  # out_features not 256 or 512
     with pytest.raises(ValueError):
         mixed_linear_residual_layer_norm(torch.zeros(4, 256, device=hip_device, dtype=torch.float16), lin,
                                          torch.zeros(4, 128, device=hip_device), norm)

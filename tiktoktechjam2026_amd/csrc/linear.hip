@@ -215,13 +215,14 @@ __device__ __forceinline__ int w_slot(int j) {
   return (j & ~31) | (((j >> 2) & 1) << 4) | ((j >> 3) & 3) << 2 | (j & 3);
 }
 
-// Large-tile projection for wide models: a 256 (tokens) x BN (features) output
-// tile per workgroup of 2 x BN/64 waves, each wave 128 x 64 (8 token tiles x 2
-// feature pairs).  K is staged in 64-wide chunks through LDS with a one-chunk
-// register prefetch: double-buffered with one barrier per chunk (STAGES == 2),
-// or single-buffered with two (STAGES == 1, half the LDS).  Each W fragment
-// read from LDS feeds 8 MFMAs and each X fragment 4; a 256 x 256 tile reads
-// 128 FLOPs' worth of operands per byte from L2, a 256 x 128 tile 85.
+// Large-tile projection for wide models: a BM (tokens) x BN (features) output
+// tile per workgroup of BM/128 x BN/64 waves, each wave 128 x 64 (8 token tiles x
+// 2 feature pairs).  K is staged in BK-wide chunks (64, or 32 where a wide tile
+// needs the LDS) through LDS with a one-chunk register prefetch: double-buffered
+// with one barrier per chunk (STAGES == 2), or single-buffered with two (STAGES
+// == 1, half the LDS).  Each W fragment read from LDS feeds 8 MFMAs and each X
+// fragment 4; a 256 x 256 tile reads 128 FLOPs' worth of operands per byte from
+// L2, a 256 x 128 tile 85, a 128 x 512 tile 102.
 //
 // The kernel is persistent: the grid fills the device once and each workgroup
 // walks a strided list of tiles inside its XCD's contiguous share of the tile
@@ -231,21 +232,30 @@ __device__ __forceinline__ int w_slot(int j) {
 // flight while the current tile's last chunk and epilogue execute, which hides
 // the load latency that short-K projections (K = 256..512) would otherwise
 // expose once per tile.
-template <int BN, int STAGES, typename XT, int EPI, typename OT>
-__global__ __launch_bounds__(2 * BN) void linear_big_kernel(LinearArgs a) {
-  constexpr int NT = 2 * BN;                    // threads: 2 x BN/64 waves
-  constexpr int BM = 256, BK = 64, LD = BK + 16;  // 160-byte rows: conflict-free b128 LDS access
+template <int BM, int BN, int BK, int STAGES, typename XT, int EPI, typename OT>
+__global__ __launch_bounds__(BM / 2 * BN / 64) void linear_big_kernel(LinearArgs a) {
   constexpr int WM = 128, WN = 64, TM = WM / 16, PN = WN / 32;
+  constexpr int WAVES_M = BM / WM;
+  constexpr int NT = 64 * WAVES_M * (BN / WN);  // threads
+  // 160-byte (BK 64) or 80-byte (BK 32) rows: the 16 rows of a b128 fragment read hit distinct banks
+  constexpr int LD = BK + (BK == 64 ? 16 : 8);
+  static_assert(BM % WM == 0 && BN % WN == 0 && (BK == 32 || BK == 64), "tile shape");
   constexpr int CPR = BK / 8;                   // 8-element chunks per staged row
   constexpr int XCH = BM * CPR / NT;            // X chunks per thread
   constexpr int WCH = BN * CPR / NT;            // W chunks per thread
   static_assert(XCH * NT == BM * CPR && WCH * NT == BN * CPR, "staging split");
   static_assert(EPI != kEpiResidualLN, "row LayerNorm needs whole rows per wave");
   static_assert(STAGES == 1 || STAGES == 2, "one or two LDS stages");
+  // LayerNorm scratch in the idle W stage: [2 passes][BN / WN][BM] partial row sums,
+  // then gamma and beta
   static_assert(EPI != kEpiResidualLNTile || STAGES == 2, "the LayerNorm epilogue uses the idle LDS stage");
+  static_assert(EPI != kEpiResidualLNTile || (2 * (BN / WN) * BM + 2 * BN) * 4 <= BN * LD * 2,
+                "LayerNorm scratch fits the idle W stage");
 
   __shared__ _Float16 xs[STAGES][BM * LD];
   __shared__ _Float16 ws[STAGES][BN * LD];
+  // LDS position (halves) of 8-element chunk c of tile row `row`
+  auto cpos = [](int row, int c) { return row * LD + 8 * c; };
 
   const XT* __restrict__ X = static_cast<const XT*>(a.x);
   const _Float16* __restrict__ W = a.w;
@@ -274,7 +284,7 @@ __global__ __launch_bounds__(2 * BN) void linear_big_kernel(LinearArgs a) {
 
   const int l = threadIdx.x & 63, wave = wave_id();
   const int r = l & 15, g = l >> 4;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
 
   f4 acc[PN][2][TM];
 #pragma unroll
@@ -317,12 +327,12 @@ __global__ __launch_bounds__(2 * BN) void linear_big_kernel(LinearArgs a) {
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
       const int c = threadIdx.x + i * NT;
-      *reinterpret_cast<h8*>(&xs[buf][(c / CPR) * LD + (c % CPR) * 8]) = xr[i];
+      *reinterpret_cast<h8*>(&xs[buf][cpos(c / CPR, c % CPR)]) = xr[i];
     }
 #pragma unroll
     for (int i = 0; i < WCH; ++i) {
       const int c = threadIdx.x + i * NT;
-      *reinterpret_cast<h8*>(&ws[buf][w_slot(c / CPR) * LD + (c % CPR) * 8]) = wr[i];
+      *reinterpret_cast<h8*>(&ws[buf][cpos(w_slot(c / CPR), c % CPR)]) = wr[i];
     }
   };
   auto compute = [&](int buf) {
@@ -336,10 +346,10 @@ __global__ __launch_bounds__(2 * BN) void linear_big_kernel(LinearArgs a) {
       for (int p = 0; p < PN; ++p)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
-          wa[p][tt] = *reinterpret_cast<const h8*>(&ws[buf][(wn * WN + 32 * p + 16 * tt + r) * LD + ks * 32 + 8 * g]);
+          wa[p][tt] = *reinterpret_cast<const h8*>(&ws[buf][cpos(wn * WN + 32 * p + 16 * tt + r, 4 * ks + g)]);
 #pragma unroll
       for (int t = 0; t < TM; ++t)
-        xb[t] = *reinterpret_cast<const h8*>(&xs[buf][(wm * WM + 16 * t + r) * LD + ks * 32 + 8 * g]);
+        xb[t] = *reinterpret_cast<const h8*>(&xs[buf][cpos(wm * WM + 16 * t + r, 4 * ks + g)]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int t = 0; t < TM; ++t)
@@ -357,8 +367,7 @@ __global__ __launch_bounds__(2 * BN) void linear_big_kernel(LinearArgs a) {
   // wave finishes the same row sums in the same order.
   auto epilogue_ln = [&](int etile, int obuf) {
     constexpr int NWN = BN / WN;  // waves across a row
-    // scratch in the idle stage: [2 passes][NWN][BM] partial row sums, then gamma and beta
-    float* red = reinterpret_cast<float*>(&xs[obuf][0]);
+    float* red = reinterpret_cast<float*>(&ws[obuf][0]);
     float* gam = red + 2 * NWN * BM;
     float* bet = gam + BN;
     const int64_t m0 = (int64_t)(etile / nbn) * BM;
@@ -542,15 +551,16 @@ static int resident_grid(Kernel kernel, int threads, size_t lds) {
   return cached[dev];
 }
 
-template <int BN, int STAGES, typename XT, int EPI, typename OT>
+template <int BM, int BN, int BK, int STAGES, typename XT, int EPI, typename OT>
 static hipError_t launch_linear_big(const LinearArgs& a, hipStream_t s) {
-  if (a.k > (1 << 20)) return (hipError_t)MPK_EUNSUPPORTED;  // 32-bit tile offsets: 256 rows x K x 4 bytes
-  const int64_t tiles = ((a.m + 255) / 256) * ((a.n + BN - 1) / BN);
+  constexpr int NT = BM / 2 * BN / 64;
+  if (a.k > (1 << 20)) return (hipError_t)MPK_EUNSUPPORTED;  // 32-bit tile offsets: BM rows x K x 4 bytes
+  const int64_t tiles = ((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
   if (tiles > 0x7fffffff) return hipErrorInvalidConfiguration;
-  auto kernel = linear_big_kernel<BN, STAGES, XT, EPI, OT>;
-  int64_t grid = std::min<int64_t>(tiles, resident_grid(kernel, 2 * BN, 0));
+  auto kernel = linear_big_kernel<BM, BN, BK, STAGES, XT, EPI, OT>;
+  int64_t grid = std::min<int64_t>(tiles, resident_grid(kernel, NT, 0));
   if (grid >= 8) grid &= ~int64_t{7};
-  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(2 * BN), 0, s, a);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(NT), 0, s, a);
   return hipGetLastError();
 }
 
@@ -579,9 +589,9 @@ static hipError_t linear_variant(int variant, const LinearArgs& a, hipStream_t s
     case 2: return launch_linear<128, 64, 64, 4, XT, EPI, OT>(a, s);
     case 3: return launch_linear<128, 32, 64, 4, XT, EPI, OT>(a, s);
     case 4: return launch_linear<64, 128, 64, 1, XT, EPI, OT>(a, s);
-    case 5: return launch_linear_big<128, 2, XT, EPI, OT>(a, s);
-    case 6: return launch_linear_big<128, 1, XT, EPI, OT>(a, s);
-    case 7: return launch_linear_big<256, 2, XT, EPI, OT>(a, s);
+    case 5: return launch_linear_big<256, 128, 64, 2, XT, EPI, OT>(a, s);
+    case 6: return launch_linear_big<256, 128, 64, 1, XT, EPI, OT>(a, s);
+    case 7: return launch_linear_big<256, 256, 64, 2, XT, EPI, OT>(a, s);
     default: return (hipError_t)MPK_EUNSUPPORTED;
   }
 }
@@ -597,10 +607,13 @@ static hipError_t linear_ln_d(int variant, const LinearArgs& a, hipStream_t s) {
 
 template <typename XT, typename OT>
 static hipError_t linear_ln(int variant, const LinearArgs& a, hipStream_t s) {
-  // variant 3: 256 x 256 GEMM tiles with the cross-wave LayerNorm epilogue (N = 256, any K)
+  // variant 3: large GEMM tiles holding whole rows, with the cross-wave LayerNorm
+  // epilogue (any K): 256 x 256 tiles for N = 256, 128 x 512 tiles (32-wide K chunks, so
+  // that two stages fit the LDS) for N = 512
   if (variant == 3) {
-    if (a.n != 256) return (hipError_t)MPK_EUNSUPPORTED;
-    return launch_linear_big<256, 2, XT, kEpiResidualLNTile, OT>(a, s);
+    if (a.n == 256) return launch_linear_big<256, 256, 64, 2, XT, kEpiResidualLNTile, OT>(a, s);
+    if (a.n == 512) return launch_linear_big<128, 512, 32, 2, XT, kEpiResidualLNTile, OT>(a, s);
+    return (hipError_t)MPK_EUNSUPPORTED;
   }
   if (a.k != a.n) return (hipError_t)MPK_EUNSUPPORTED;
   switch (a.n) {
@@ -713,7 +726,7 @@ extern "C" int mpk_linear_add_layernorm(const void* x, int x_dtype, const void* 
     return MPK_EINVAL;
   if ((x_dtype != kF32 && x_dtype != kF16) || (normalized_dtype != kF32 && normalized_dtype != kF16))
     return MPK_EINVAL;
-  if (n != 256 || k % 8 != 0) return MPK_EUNSUPPORTED;
+  if ((n != 256 && n != 512) || k % 8 != 0) return MPK_EUNSUPPORTED;
   if (!aligned16(x) || !aligned16(w) || !aligned16(b) || !aligned16(residual) || !aligned16(gamma) ||
       !aligned16(beta) || !aligned16(residual_out) || !aligned16(normalized_out))
     return MPK_EALIGN;

@@ -19,11 +19,15 @@ the shape is only
   measured on MI355X (256 CUs, 64-lane waves); a ``Route`` can pin a variant
   per launch (tests and sweeps do).
 
-At d_model 256 (``WIDE_LN_EPILOGUE_WIDTH``) the GEMM route's two residual
-projections carry the next LayerNorm in their epilogue (``wide_ln_epilogue``):
-a 256 x 256 output tile holds whole rows, so the row statistics are exchanged
-across its waves in LDS and no separate LayerNorm launch re-reads the residual
-stream.
+At d_model 256 and 512 (``WIDE_LN_EPILOGUE_WIDTHS``) the GEMM route's
+out-projection carries the next LayerNorm in its epilogue (``wide_ln_epilogue``):
+a 256 x 256 (d 256) or 128 x 512 (d 512) output tile holds whole rows, so the row
+statistics are exchanged across its waves in LDS and no separate LayerNorm launch
+re-reads the residual stream.  The FFN-output projection does the same at d_model
+256 (``wide_ln_ffn_out``); at 512 its K = ffn_dim loop runs faster on 256 x 256
+tiles with 64-wide K chunks than on the LDS-limited 128 x 512 LayerNorm tile
+(32-wide chunks: 142 vs 113 us with the separate LayerNorm at cfg4), so it keeps
+the separate LayerNorm there.
 
 At d_model 256 the FFN runs as one kernel too (``WIDE_FFN_WIDTH``,
 ``fuse_full_ffn``): both products on 32x32 MFMAs with the hidden activation in
@@ -63,8 +67,11 @@ LAYER_TAIL_SHAPES = frozenset({(32, 32), (32, 64), (32, 128), (64, 64), (64, 128
 LAYERNORM_QKV_WIDTHS = frozenset({32, 64, 128})
 # From this width up the out-projection and FFN run as GEMMs + a separate LayerNorm.
 WIDE_GEMM_FROM = 256
-# GEMM-route width whose residual projections fuse the next LayerNorm (256 x 256 tiles).
-WIDE_LN_EPILOGUE_WIDTH = 256
+# GEMM-route widths whose out-projection fuses the next LayerNorm (tiles holding whole
+# rows); must equal the widths mpk_linear_add_layernorm accepts.  The FFN-output
+# projection fuses it at the widths of WIDE_LN_FFN_OUT_WIDTHS.
+WIDE_LN_EPILOGUE_WIDTHS = (256, 512)
+WIDE_LN_FFN_OUT_WIDTHS = (256,)
 # Width of the wide fused FFN kernel (32x32-MFMA, hidden on chip) and its largest ffn_dim;
 # must equal ffn_wide_supported in the library.
 WIDE_FFN_WIDTH = 256
@@ -83,6 +90,7 @@ class Route:
     fuse_full_ffn: bool = True
     fuse_layer_tail: bool = False
     wide_ln_epilogue: bool = False
+    wide_ln_ffn_out: bool = False
     qkv_variant: int = 0
     attention_variant: int = 0
     out_ln_variant: int = 0
@@ -104,6 +112,7 @@ class Route:
             "full_ffn_fusion": self.fuse_full_ffn,
             "layer_tail_fusion": self.fuse_layer_tail,
             "wide_ln_epilogue": self.wide_ln_epilogue,
+            "wide_ln_ffn_out": self.wide_ln_ffn_out,
             "variants": {
                 "qkv": self.qkv_variant,
                 "attention": self.attention_variant,
@@ -151,7 +160,7 @@ def plan(
     )
     wide_ln = (
         enable_attention_output_norm_fusion and enable_full_ffn_fusion and not narrow
-        and d == WIDE_LN_EPILOGUE_WIDTH
+        and d in WIDE_LN_EPILOGUE_WIDTHS
     )
     route = Route(
         True,
@@ -162,5 +171,6 @@ def plan(
         fuse_full_ffn=fuse_ffn,
         fuse_layer_tail=fuse_tail,
         wide_ln_epilogue=wide_ln,
+        wide_ln_ffn_out=wide_ln and d in WIDE_LN_FFN_OUT_WIDTHS,
     )
     return route

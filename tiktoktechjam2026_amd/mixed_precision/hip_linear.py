@@ -159,7 +159,7 @@ def mixed_linear_add_layer_norm(
     )
 
 
-WIDE_LN_EPILOGUE_WIDTH = 256
+WIDE_LN_EPILOGUE_WIDTHS = (256, 512)
 
 
 def mixed_linear_residual_layer_norm(
@@ -175,8 +175,9 @@ def mixed_linear_residual_layer_norm(
     The wide-route counterpart of ``mixed_linear_add_layer_norm`` (whose
     projection is square): the out-projection or the FFN-output projection,
     its residual add and the next LayerNorm (reference generic route,
-    ``mixed_precision/transformer.py:664-690``) run as one kernel on 256 x 256
-    GEMM tiles.  ``linear.out_features`` must be 256.  Returns ``(R', N')``.
+    ``mixed_precision/transformer.py:664-690``) run as one kernel on GEMM tiles
+    that hold whole rows.  ``linear.out_features`` must be 256 or 512.  Returns
+    ``(R', N')``.
     """
     n_features = linear.out_features
     if not (
@@ -187,7 +188,8 @@ def mixed_linear_residual_layer_norm(
         and x.shape[:-1] == residual.shape[:-1]
         and x.shape[-1] == linear.in_features
         and linear.in_features % 8 == 0
-        and residual.shape[-1] == n_features == WIDE_LN_EPILOGUE_WIDTH
+        and residual.shape[-1] == n_features
+        and n_features in WIDE_LN_EPILOGUE_WIDTHS
         and _fp16_linear_ok(linear)
         and _norm_ok(norm, n_features)
         and normalized_dtype in (torch.float16, torch.float32)

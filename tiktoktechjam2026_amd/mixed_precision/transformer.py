@@ -147,7 +147,7 @@ class MixedPrecisionTransformerBlock(nn.Module):
         activated = mixed_linear(
             normalized_ffn, self.ffn_in, output_dtype=torch.float16, fuse_gelu=True, variant=route.ffn_in_variant
         )
-        if route.wide_ln_epilogue:
+        if route.wide_ln_ffn_out:
             return mixed_linear_residual_layer_norm(
                 activated, self.ffn_out, residual, next_norm, normalized_dtype=out_dtype
             )

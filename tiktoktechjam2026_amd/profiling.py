@@ -84,8 +84,10 @@ def forward_costs(config, normalized_bytes: int = 2, route=None) -> Dict[str, Ke
             ),
         }
     wide_ln = getattr(route, "wide_ln_epilogue", False)
-    norm_launches = 1 if wide_ln else (
-        1 + (0 if route.fuse_attention_output_norm else L) + (0 if route.fuse_full_ffn else L)
+    wide_ln_ffn = getattr(route, "wide_ln_ffn_out", False)
+    norm_launches = (
+        1 + (0 if route.fuse_attention_output_norm or wide_ln else L)
+        + (0 if route.fuse_full_ffn or wide_ln_ffn else L)
     )
     costs = {
         "layernorm": KernelCost("layernorm", norm_launches, 0.0, M * D * (4 + sn)),
@@ -93,7 +95,7 @@ def forward_costs(config, normalized_bytes: int = 2, route=None) -> Dict[str, Ke
         "attention": attention,
     }
     if wide_ln:
-        # residual projections with the next LayerNorm in the epilogue (256 x 256 GEMM tiles)
+        # residual projection with the next LayerNorm in the epilogue (tiles of whole rows)
         costs["out_proj_ln"] = KernelCost(
             "out_proj_ln", L, 2.0 * M * D * D, M * D * 2 + 2 * D * D + 2 * D + 8 * M * D + M * D * sn + 8 * D
         )
@@ -107,7 +109,7 @@ def forward_costs(config, normalized_bytes: int = 2, route=None) -> Dict[str, Ke
         )
     if route.fuse_full_ffn:
         costs["ffn_ln"] = KernelCost("ffn_ln", L, 4.0 * M * D * F, M * D * sn + 4 * D * F + M * D * (8 + sn))
-    elif wide_ln:
+    elif wide_ln_ffn:
         costs["ffn_in"] = KernelCost("ffn_in", L, 2.0 * M * D * F, M * D * sn + 2 * D * F + 2 * F + M * F * 2)
         # the last layer's normalized output is FP32 (counted at the stream width here)
         costs["ffn_out_ln"] = KernelCost(
