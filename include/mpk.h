@@ -149,7 +149,9 @@ int mpk_attention_auto_variant(int32_t batch, int32_t heads, int32_t seq_len, in
  *   last != 0: out = LayerNorm(x_out; next_ln)                      (FP32 [m, d])
  * ctx: [m, d] FP16; x, x_out: [m, d] FP32 (may not alias); w_o [d, d], w_in [f, d],
  * w_out [d, f], w_qkv [3d, d] and their biases FP16; LayerNorm parameters FP32.
- * (d, f) must satisfy mpk_layer_tail_supported.
+ * (d, f) must satisfy mpk_layer_tail_supported.  variant: 0 = built-in choice (3 when
+ * 128-row tiles would leave CUs idle, else 1), 1 = 8 waves x 16 rows per workgroup,
+ * 2 = 8 waves x 32 rows (where its LDS footprint fits, else as 1), 3 = 4 waves x 16 rows.
  * Replaces, fused: mixed_linear_add_layer_norm + mixed_ffn_add_layer_norm +
  * the next layer's mixed_linear QKV call (mixed_precision/transformer.py:196-222,
  * :540-560, :88-120); no single reference function corresponds to it.
@@ -163,7 +165,8 @@ int mpk_layer_tail_supported(int32_t d, int32_t f);
 
 /*
  * First-layer head: qkv = LayerNorm(x; ln_w, ln_b, eps) w_qkv^T + b_qkv.
- * x: [m, d] FP32; w_qkv: [3d, d] FP16; b_qkv: [3d] FP16; qkv: [m, 3d] FP16.
+ * x: [m, d] FP32; w_qkv: [3d, d] FP16; b_qkv: [3d] FP16; qkv: [m, 3d] FP16.  variant as
+ * for mpk_layer_tail.
  * Replaces, fused: the initial norm1 + cast (mixed_precision/transformer.py:484-486)
  * and the first layer's QKV mixed_linear (:88-120).
  */

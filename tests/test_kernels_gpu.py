@@ -508,7 +508,7 @@ def _ln_module_ref(r64, norm):
 
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("m", [5, 1000, 9000])
-@pytest.mark.parametrize("variant", [1, 2])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
 def test_layer_norm_qkv(hip_device, d, m, variant):
     from tiktoktechjam2026_amd.mixed_precision.hip_fused import layer_norm_qkv
 
@@ -526,17 +526,18 @@ def test_layer_norm_qkv(hip_device, d, m, variant):
 @pytest.mark.parametrize("d,f", [(128, 128), (32, 64), (64, 256), (32, 32)])
 @pytest.mark.parametrize("m", [7, 4100])
 @pytest.mark.parametrize("last", [False, True])
-@pytest.mark.parametrize("variant", [1, 2])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
 def test_fused_layer_tail(hip_device, d, f, m, last, variant):
     _check_layer_tail(hip_device, d, f, m, last, variant)
 
 
 # Row counts that give every workgroup of the persistent grid at least two tiles, with a
-# ragged last tile on the second pass (d 32/64: 512 workgroups x 128 rows; d 128: 256 x 128).
+# ragged last tile on the second pass (d 32/64: 512 workgroups x 128 rows; d 128: 256 x 128;
+# variant 3 has 64-row tiles, so the same counts give it four or more passes).
 @pytest.mark.parametrize("d,f,m", [(32, 64, 2 * 512 * 128 + 37), (64, 256, 2 * 512 * 128 + 37),
                                    (128, 128, 2 * 256 * 128 + 37)])
 @pytest.mark.parametrize("last", [False, True])
-@pytest.mark.parametrize("variant", [1, 2])
+@pytest.mark.parametrize("variant", [1, 2, 3])
 def test_fused_layer_tail_multi_pass(hip_device, d, f, m, last, variant):
     _check_layer_tail(hip_device, d, f, m, last, variant)
 

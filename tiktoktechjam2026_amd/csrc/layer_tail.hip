@@ -55,8 +55,6 @@ struct TailArgs {
   float eps2, eps1;
 };
 
-constexpr int kTailWaves = 8;
-constexpr int kTailThreads = 64 * kTailWaves;
 constexpr int kLdsBudget = 160 * 1024;
 
 // Where the next layer's QKV weights live.
@@ -66,7 +64,8 @@ constexpr int kLdsBudget = 160 * 1024;
 //            are exchanged through LDS and every wave projects all of them.
 enum QkvMode : int { kQkvLds = 1, kQkvReg = 2 };
 
-template <int D, int F, int TM, bool STAGE1, bool QKV, int QMODE>
+// W: waves per workgroup (8, or 4 where 8-wave tiles would leave CUs idle).
+template <int D, int F, int TM, bool STAGE1, bool QKV, int QMODE, int W>
 struct TailShape {
   static constexpr int LDD = D + 8;  // row stride of [*, D] tiles (halves)
   static constexpr int LDF = F + 8;  // row stride of Wout [D, F] (halves)
@@ -75,7 +74,7 @@ struct TailShape {
   static constexpr int WOUT = WIN + (STAGE1 ? F * LDD : 0);
   static constexpr int WQKV = WOUT + (STAGE1 ? D * LDF : 0);
   static constexpr int NBUF = WQKV + (QKV && QMODE == kQkvLds ? 3 * D * LDD : 0);
-  static constexpr int TOTAL = NBUF + (QKV && QMODE == kQkvReg ? 16 * TM * kTailWaves * LDD : 0);
+  static constexpr int TOTAL = NBUF + (QKV && QMODE == kQkvReg ? 16 * TM * W * LDD : 0);
   // Small per-feature parameters, staged once per workgroup as FP32 after the
   // FP16 region (offsets in floats): b_o, LN2 gamma/beta, b_in, b_out (STAGE1),
   // the next LayerNorm's gamma/beta, and b_qkv (QKV).
@@ -95,17 +94,17 @@ struct TailShape {
 // Two-phase staging of a [ROWS, COLS] FP16 matrix into LDS (row stride LD): load()
 // issues all of this thread's global reads, store() writes them to LDS, so the
 // reads of every staged array can be in flight together.
-template <int ROWS, int COLS, int LD, bool ON>
+template <int ROWS, int COLS, int LD, bool ON, int NT>
 struct MatStage {
   static constexpr int CPR = COLS / 8;
   static constexpr int CHUNKS = ON ? ROWS * CPR : 0;
-  static constexpr int PER = ON ? (CHUNKS + kTailThreads - 1) / kTailThreads : 1;
+  static constexpr int PER = ON ? (CHUNKS + NT - 1) / NT : 1;
   h8 v[PER];
   __device__ __forceinline__ void load(const _Float16* src) {
     if constexpr (ON) {
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
-        const int c = threadIdx.x + i * kTailThreads;
+        const int c = threadIdx.x + i * NT;
         if (c < CHUNKS) v[i] = *reinterpret_cast<const h8*>(&src[(int64_t)(c / CPR) * COLS + (c % CPR) * 8]);
       }
     }
@@ -114,22 +113,26 @@ struct MatStage {
     if constexpr (ON) {
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
-        const int c = threadIdx.x + i * kTailThreads;
+        const int c = threadIdx.x + i * NT;
         if (c < CHUNKS) *reinterpret_cast<h8*>(&dst[(c / CPR) * LD + (c % CPR) * 8]) = v[i];
       }
     }
   }
 };
 
-// Two-phase staging of n (1 <= n <= kTailThreads) FP16 or FP32 parameters as FP32.
-// The read is unconditional (threads past n re-read element n - 1), so no
-// branch separates it from the other prologue reads.
-template <typename T>
+// Two-phase staging of n (1 <= n <= 2 NT) FP16 or FP32 parameters as FP32, up to two
+// per thread.  The reads are unconditional (threads past n re-read element n - 1), so
+// no branch separates them from the other prologue reads.
+template <typename T, int NT>
 struct ParamStage {
-  T v;
-  __device__ __forceinline__ void load(const T* src, int n) { v = src[min((int)threadIdx.x, n - 1)]; }
+  T v[2];
+  __device__ __forceinline__ void load(const T* src, int n) {
+    v[0] = src[min((int)threadIdx.x, n - 1)];
+    v[1] = src[min((int)threadIdx.x + NT, n - 1)];
+  }
   __device__ __forceinline__ void store(float* dst, int n) const {
-    if ((int)threadIdx.x < n) dst[threadIdx.x] = (float)v;
+    if ((int)threadIdx.x < n) dst[threadIdx.x] = (float)v[0];
+    if ((int)threadIdx.x + NT < n) dst[threadIdx.x + NT] = (float)v[1];
   }
 };
 
@@ -197,19 +200,20 @@ __device__ __forceinline__ void load_tile(TileIn<D, TM, STAGE1>& in, const TailA
   }
 }
 
-template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE>
-__global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
+template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE, int W>
+__global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
   constexpr bool QKV = !LAST;
-  using SH = TailShape<D, F, TM, STAGE1, QKV, QMODE>;
+  constexpr int NT = 64 * W;
+  using SH = TailShape<D, F, TM, STAGE1, QKV, QMODE, W>;
   constexpr int PN = D / 32;   // feature pairs of a D-wide row
   constexpr int KS = D / 32;   // k-steps over D
   constexpr int FQ = F / 32;   // hidden feature pairs
   constexpr int QP = 3 * D / 32;
-  constexpr int ROWS = 16 * TM * kTailWaves;
-  constexpr int QNW = 3 * D / kTailWaves;  // QKV columns per wave (register mode)
+  constexpr int ROWS = 16 * TM * W;
+  constexpr int QNW = 3 * D / W;           // QKV columns per wave (register mode)
   constexpr int QNT = QNW / 16;            // 16-column tiles per wave (register mode)
   static_assert(D % 32 == 0 && F % 32 == 0, "shape");
-  static_assert(QMODE != kQkvReg || QNT * 16 * kTailWaves == 3 * D, "register mode needs 3D/16 divisible by 8");
+  static_assert(QMODE != kQkvReg || QNT * 16 * W == 3 * D, "register mode needs 3D/16 divisible by W");
 
   extern __shared__ __align__(16) _Float16 lds[];
 
@@ -218,16 +222,16 @@ __global__ __launch_bounds__(kTailThreads) void layer_tail_kernel(TailArgs a) {
 
   // Prologue: every global read (weights, parameters, the register-resident QKV
   // weights) is issued before the first LDS write, so it costs one memory latency.
-  static_assert(3 * D <= kTailThreads && F <= kTailThreads, "one parameter per thread");
-  MatStage<D, D, SH::LDD, STAGE1> s_wo;
-  MatStage<F, D, SH::LDD, STAGE1> s_win;
-  MatStage<D, F, SH::LDF, STAGE1> s_wout;
-  MatStage<3 * D, D, SH::LDD, QKV && QMODE == kQkvLds> s_wqkv;
+  static_assert(3 * D <= 2 * NT && F <= 2 * NT, "two parameters per thread");
+  MatStage<D, D, SH::LDD, STAGE1, NT> s_wo;
+  MatStage<F, D, SH::LDD, STAGE1, NT> s_win;
+  MatStage<D, F, SH::LDF, STAGE1, NT> s_wout;
+  MatStage<3 * D, D, SH::LDD, QKV && QMODE == kQkvLds, NT> s_wqkv;
   // Biases, gammas and betas live in LDS for the whole kernel: read inside the
   // per-tile dependency chain, global loads would put a memory latency between
   // every product and its epilogue.
-  ParamStage<_Float16> p_bo, p_bin, p_bout, p_bqkv;
-  ParamStage<float> p_g2, p_be2, p_g1, p_be1;
+  ParamStage<_Float16, NT> p_bo, p_bin, p_bout, p_bqkv;
+  ParamStage<float, NT> p_g2, p_be2, p_g1, p_be1;
   if constexpr (STAGE1) {
     p_bo.load(a.bo, D);
     p_g2.load(a.g2, D);
@@ -544,12 +548,12 @@ static int tail_cu_count() {
   return cached[dev];
 }
 
-template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE>
+template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE, int W>
 static hipError_t launch_tail(const TailArgs& a, hipStream_t s) {
-  using SH = TailShape<D, F, TM, STAGE1, !LAST, QMODE>;
+  using SH = TailShape<D, F, TM, STAGE1, !LAST, QMODE, W>;
   constexpr int lds_bytes = SH::BYTES;
   static_assert(lds_bytes <= kLdsBudget, "weights exceed LDS");
-  auto kern = layer_tail_kernel<D, F, TM, STAGE1, LAST, QMODE>;
+  auto kern = layer_tail_kernel<D, F, TM, STAGE1, LAST, QMODE, W>;
   if (lds_bytes > 64 * 1024) {
     static std::atomic<bool> attribute_set{false};  // once per instantiation
     if (!attribute_set.load(std::memory_order_acquire)) {
@@ -559,31 +563,38 @@ static hipError_t launch_tail(const TailArgs& a, hipStream_t s) {
       attribute_set.store(true, std::memory_order_release);
     }
   }
-  constexpr int ROWS = 16 * TM * kTailWaves;
+  constexpr int ROWS = 16 * TM * W;
   const int64_t ntiles = (a.m + ROWS - 1) / ROWS;
   const int64_t per_cu = lds_bytes > kLdsBudget / 2 ? 1 : 2;
   int64_t grid = (int64_t)tail_cu_count() * per_cu;
   if (grid > ntiles) grid = ntiles;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kTailThreads), lds_bytes, s, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * W), lds_bytes, s, a);
   return hipGetLastError();
 }
 
 // QKV weights in LDS when the whole set fits, else stationary in registers.
 template <int D, int F, bool STAGE1>
 constexpr int qkv_mode() {
-  return TailShape<D, F, 1, STAGE1, true, kQkvLds>::BYTES <= kLdsBudget ? kQkvLds : kQkvReg;
+  return TailShape<D, F, 1, STAGE1, true, kQkvLds, 8>::BYTES <= kLdsBudget ? kQkvLds : kQkvReg;
 }
 
+// Variants: 1: 8 waves x 16 rows (128-row tiles); 2: 8 waves x 32 rows, where its LDS
+// footprint fits; 3: 4 waves x 16 rows (64-row tiles), for row counts whose 128-row
+// tiles would leave CUs idle.
 template <int D, int F, bool STAGE1>
 static hipError_t tail_variant(int variant, bool last, const TailArgs& a, hipStream_t s) {
   constexpr int QM = qkv_mode<D, F, STAGE1>();
-  // variant 2 (32 rows per wave) only where its LDS footprint still fits
-  if constexpr (TailShape<D, F, 2, STAGE1, true, QM>::BYTES <= kLdsBudget) {
+  if constexpr (TailShape<D, F, 2, STAGE1, true, QM, 8>::BYTES <= kLdsBudget) {
     if (variant == 2)
-      return last ? launch_tail<D, F, 2, STAGE1, true, QM>(a, s) : launch_tail<D, F, 2, STAGE1, false, QM>(a, s);
+      return last ? launch_tail<D, F, 2, STAGE1, true, QM, 8>(a, s) : launch_tail<D, F, 2, STAGE1, false, QM, 8>(a, s);
   }
-  return last ? launch_tail<D, F, 1, STAGE1, true, QM>(a, s) : launch_tail<D, F, 1, STAGE1, false, QM>(a, s);
+  if (variant == 3)
+    return last ? launch_tail<D, F, 1, STAGE1, true, QM, 4>(a, s) : launch_tail<D, F, 1, STAGE1, false, QM, 4>(a, s);
+  return last ? launch_tail<D, F, 1, STAGE1, true, QM, 8>(a, s) : launch_tail<D, F, 1, STAGE1, false, QM, 8>(a, s);
 }
+
+// 64-row tiles when 128-row tiles would not give every CU one
+static int tail_auto_variant(int64_t m) { return (m + 127) / 128 < tail_cu_count() ? 3 : 1; }
 
 }  // namespace mpk
 
@@ -611,8 +622,8 @@ extern "C" int mpk_layer_tail(const void* ctx, const float* x, const void* w_o, 
     if (!aligned16(p)) return MPK_EALIGN;
   if (!last && (!aligned16(w_qkv) || !aligned16(b_qkv))) return MPK_EALIGN;
   if (m == 0) return MPK_OK;
-  if (variant == 0) variant = 1;
-  if (variant != 1 && variant != 2) return MPK_EUNSUPPORTED;
+  if (variant == 0) variant = tail_auto_variant(m);
+  if (variant < 1 || variant > 3) return MPK_EUNSUPPORTED;
   TailArgs a{};
   a.ctx = static_cast<const _Float16*>(ctx); a.x = x;
   a.wo = static_cast<const _Float16*>(w_o); a.bo = static_cast<const _Float16*>(b_o); a.g2 = ln2_w; a.be2 = ln2_b;
@@ -645,8 +656,8 @@ extern "C" int mpk_layernorm_qkv(const float* x, const float* ln_w, const float*
   for (const void* p : ptrs)
     if (!aligned16(p)) return MPK_EALIGN;
   if (m == 0) return MPK_OK;
-  if (variant == 0) variant = 1;
-  if (variant != 1 && variant != 2) return MPK_EUNSUPPORTED;
+  if (variant == 0) variant = tail_auto_variant(m);
+  if (variant < 1 || variant > 3) return MPK_EUNSUPPORTED;
   TailArgs a{};
   a.x = x; a.g1 = ln_w; a.be1 = ln_b;
   a.wqkv = static_cast<const _Float16*>(w_qkv); a.bqkv = static_cast<const _Float16*>(b_qkv);
