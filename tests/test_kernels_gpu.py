@@ -291,17 +291,20 @@ def test_ffn_residual_layernorm(hip_device, d, f, m, variant):
     _check_ffn(hip_device, d, f, m, variant, torch.float16)
 
 
-# The wide kernel (variant 3, d_model 256): one chunk (f 32), no steady chunk (f 64), odd chunk
-# counts, the cfg5 shape; row counts below one tile, ragged, and with two or more tiles per
-# workgroup of the persistent grid (256 workgroups x 128 rows per pass) and a ragged last tile.
+# The wide kernels (d_model 256; variant 3 one wave per SIMD, variant 4 paired waves): one
+# chunk (f 32), no steady chunk (f 64), odd chunk counts, the cfg5 shape; row counts below one
+# tile, ragged, and with two or more tiles per workgroup of the persistent grid (256
+# workgroups x 128 rows per pass) and a ragged last tile.
+@pytest.mark.parametrize("variant", [3, 4])
 @pytest.mark.parametrize("f", [32, 64, 96, 1024])
 @pytest.mark.parametrize("m", [9, 3000, 2 * 256 * 128 + 37])
-def test_ffn_wide_residual_layernorm(hip_device, f, m):
-    _check_ffn(hip_device, 256, f, m, 3, torch.float16)
+def test_ffn_wide_residual_layernorm(hip_device, f, m, variant):
+    _check_ffn(hip_device, 256, f, m, variant, torch.float16)
 
 
-def test_ffn_wide_fp32_input(hip_device):
-    _check_ffn(hip_device, 256, 1024, 777, 3, torch.float32)
+@pytest.mark.parametrize("variant", [3, 4])
+def test_ffn_wide_fp32_input(hip_device, variant):
+    _check_ffn(hip_device, 256, 1024, 777, variant, torch.float32)
 
 
 def _check_ffn(hip_device, d, f, m, variant, x_dtype):

@@ -224,6 +224,9 @@ static hipError_t ffn_dispatch(int variant, const FfnArgs& a, int d, hipStream_t
   // variant 3: the wide kernel (d_model 256, 32x32x16 MFMAs, 128-token workgroups)
   if (variant == 3) return launch_ffn_wide(a, d, kF16, std::is_same<XT, float>::value ? kF32 : kF16,
                                            std::is_same<OT, float>::value ? kF32 : kF16, s);
+  // variant 4: the paired-wave wide kernel (d_model 256, 16x16x32 MFMAs, two waves per SIMD)
+  if (variant == 4) return launch_ffn_pair(a, d, kF16, std::is_same<XT, float>::value ? kF32 : kF16,
+                                           std::is_same<OT, float>::value ? kF32 : kF16, s);
   // variant 1: TM=1; variant 2: TM=2 (D <= 256)
   const bool two = variant == 2;
   switch (d) {
@@ -266,7 +269,7 @@ extern "C" int mpk_ffn_residual_layernorm(const void* x, int x_dtype, const void
     return MPK_EALIGN;
   if (m == 0) return MPK_OK;
   if (variant == 0) variant = mpk_ffn_residual_layernorm_auto_variant(m, d, f);
-  if (variant < 1 || variant > 3) return MPK_EUNSUPPORTED;
+  if (variant < 1 || variant > 4) return MPK_EUNSUPPORTED;
   FfnArgs a{};
   a.x = x; a.w_in = static_cast<const _Float16*>(w_in); a.b_in = static_cast<const _Float16*>(b_in);
   a.w_out = static_cast<const _Float16*>(w_out); a.b_out = static_cast<const _Float16*>(b_out);
