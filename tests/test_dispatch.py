@@ -78,11 +78,12 @@ def test_python_tables_match_library(built_library):
         assert bool(lib.mpk_layernorm_qkv_supported(d)) == (d in dispatch.LAYERNORM_QKV_WIDTHS)
         for f in (32, 64, 96, 128, 256, 512, 1024, 2048):
             assert bool(lib.mpk_layer_tail_supported(d, f)) == ((d, f) in dispatch.LAYER_TAIL_SHAPES)
-    # the wide fused FFN (variant 3) is the library's choice exactly where the route fuses it
+    # the wide fused FFN (variant 4, the role-split kernel) is the library's choice exactly
+    # where the route fuses it
     for d in (128, 256, 512):
         for f in (32, 96, 1024, dispatch.WIDE_FFN_MAX_F, dispatch.WIDE_FFN_MAX_F + 32):
             wide = d == dispatch.WIDE_FFN_WIDTH and f <= dispatch.WIDE_FFN_MAX_F
-            assert (lib.mpk_ffn_residual_layernorm_auto_variant(65536, d, f) == 3) == wide, (d, f)
+            assert (lib.mpk_ffn_residual_layernorm_auto_variant(65536, d, f) == 4) == wide, (d, f)
 
 
 def test_model_interface_mirrors_reference():

@@ -291,10 +291,10 @@ def test_ffn_residual_layernorm(hip_device, d, f, m, variant):
     _check_ffn(hip_device, d, f, m, variant, torch.float16)
 
 
-# The wide kernels (d_model 256; variant 3 one wave per SIMD, variant 4 paired waves): one
-# chunk (f 32), no steady chunk (f 64), odd chunk counts, the cfg5 shape; row counts below one
-# tile, ragged, and with two or more tiles per workgroup of the persistent grid (256
-# workgroups x 128 rows per pass) and a ragged last tile.
+# The wide kernels (d_model 256; variant 3 one wave per SIMD, variant 4 vector + matrix
+# waves): one chunk (f 32), no steady chunk (f 64), odd chunk counts, the cfg5 shape; row
+# counts below one tile, ragged, and with two or more tiles per workgroup of the persistent
+# grid (256 workgroups x 128 rows per pass) and a ragged last tile.
 @pytest.mark.parametrize("variant", [3, 4])
 @pytest.mark.parametrize("f", [32, 64, 96, 1024])
 @pytest.mark.parametrize("m", [9, 3000, 2 * 256 * 128 + 37])

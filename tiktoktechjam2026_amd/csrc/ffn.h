@@ -28,7 +28,7 @@ constexpr int kWideFfnMaxF = 8192;
 // (x_dtype / out_dtype: kF32 or kF16; w_dtype is always kF16).
 bool ffn_wide_supported(int d, int f);
 hipError_t launch_ffn_wide(const FfnArgs& a, int d, int w_dtype, int x_dtype, int out_dtype, hipStream_t s);
-// The paired-wave wide kernel (two waves per SIMD; same shapes as ffn_wide_supported).
-hipError_t launch_ffn_pair(const FfnArgs& a, int d, int w_dtype, int x_dtype, int out_dtype, hipStream_t s);
+// The role-split wide kernel (vector waves + matrix waves; same shapes as ffn_wide_supported).
+hipError_t launch_ffn_roles(const FfnArgs& a, int d, int w_dtype, int x_dtype, int out_dtype, hipStream_t s);
 
 }  // namespace mpk

@@ -224,9 +224,9 @@ static hipError_t ffn_dispatch(int variant, const FfnArgs& a, int d, hipStream_t
   // variant 3: the wide kernel (d_model 256, 32x32x16 MFMAs, 128-token workgroups)
   if (variant == 3) return launch_ffn_wide(a, d, kF16, std::is_same<XT, float>::value ? kF32 : kF16,
                                            std::is_same<OT, float>::value ? kF32 : kF16, s);
-  // variant 4: the paired-wave wide kernel (d_model 256, 16x16x32 MFMAs, two waves per SIMD)
-  if (variant == 4) return launch_ffn_pair(a, d, kF16, std::is_same<XT, float>::value ? kF32 : kF16,
-                                           std::is_same<OT, float>::value ? kF32 : kF16, s);
+  // variant 4: the role-split wide kernel (d_model 256, vector and matrix waves)
+  if (variant == 4) return launch_ffn_roles(a, d, kF16, std::is_same<XT, float>::value ? kF32 : kF16,
+                                            std::is_same<OT, float>::value ? kF32 : kF16, s);
   // variant 1: TM=1; variant 2: TM=2 (D <= 256)
   const bool two = variant == 2;
   switch (d) {
@@ -246,7 +246,7 @@ using namespace mpk;
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 extern "C" int mpk_ffn_residual_layernorm_auto_variant(int64_t m, int32_t d, int32_t f) {
-  if (ffn_wide_supported(d, f)) return 3;
+  if (ffn_wide_supported(d, f)) return 4;
   if (d <= 128 && m >= 64 * 1024) return 2;
   return 1;
 }
