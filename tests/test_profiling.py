@@ -21,6 +21,18 @@ HEAD = "_ZN3mpk17layer_tail_kernelILi128ELi32ELi1ELb0ELb0ELi1EEEvNS_8TailArgsE"
 COPY = "__amd_rocclr_copyBuffer"
 
 
+# the current template layout <BM, BN, BK, STAGES, XT, EPI, OT> and the role-split FFN
+BIG_LN_512 = "_ZN3mpk17linear_big_kernelILi128ELi512ELi32ELi2EDF16_Li4EDF16_EEvNS_10LinearArgsE"
+BIG_QKV_256 = "_ZN3mpk17linear_big_kernelILi256ELi256ELi64ELi2EDF16_Li0EDF16_EEvNS_10LinearArgsE"
+FFN_ROLES = "_ZN3mpk16ffn_roles_kernelILi256EDF16_DF16_EEvNS_7FfnArgsE"
+
+
+def test_roles_of_current_kernel_templates():
+    assert profiling.parse_kernel_name(BIG_LN_512) == (
+        "linear_big_kernel", ["128", "512", "32", "2", "_Float16", "4", "_Float16"])
+    assert [profiling.base_kernel_key(n) for n in (BIG_LN_512, BIG_QKV_256, FFN_ROLES)] == ["@ln", "qkv_proj", "ffn_ln"]
+
+
 def test_parse_mangled_and_demangled_names():
     assert profiling.parse_kernel_name(BIG_LN) == ("linear_big_kernel", ["256", "2", "_Float16", "4", "_Float16"])
     assert profiling.parse_kernel_name(ATTN)[1][-1] == "false"

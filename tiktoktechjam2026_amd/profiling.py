@@ -340,10 +340,12 @@ def base_kernel_key(name: str) -> str:
     if base in ("attention32_kernel", "attention_kernel"):
         return "attention"
     if base in ("linear_big_kernel", "linear_kernel"):
-        index = 3 if base == "linear_big_kernel" else 5
-        epi = int(args[index]) if len(args) > index and args[index].lstrip("-").isdigit() else -1
+        # the epilogue is the integer template argument that follows the input type
+        types = [i for i, a in enumerate(args) if a in ("float", "_Float16")]
+        index = types[0] + 1 if types else -1
+        epi = int(args[index]) if 0 <= index < len(args) and args[index].lstrip("-").isdigit() else -1
         return {0: "qkv_proj", 1: "ffn_in", 2: "@ln", 3: "@residual", 4: "@ln"}.get(epi, "linear")
-    if base in ("ffn_ln_kernel", "ffn_wide_kernel"):
+    if base in ("ffn_ln_kernel", "ffn_wide_kernel", "ffn_roles_kernel"):
         return "ffn_ln"
     if base == "residual_layernorm_kernel":
         return "layernorm"
