@@ -111,7 +111,7 @@ def _ref_linear(x, lin, gelu):
     [(8192, 384, 128), (1000, 96, 32), (333, 2048, 512), (5, 64, 64), (4096, 128, 128), (130, 768, 256),
      (257, 40, 24)],
 )
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6, 7, 8])
 def test_mixed_linear(hip_device, m, n, k, variant):
     from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear
 
@@ -161,7 +161,7 @@ def test_gelu_epilogue_accuracy(hip_device, n, variant):
 @pytest.mark.parametrize(
     "m,n,k", [(8192, 512, 2048), (777, 256, 256), (3, 136, 40), (70000, 128, 512), (4100, 1024, 264)]
 )
-@pytest.mark.parametrize("variant", [0, 1, 5, 6, 7])
+@pytest.mark.parametrize("variant", [0, 1, 5, 6, 7, 8])
 def test_mixed_linear_residual(hip_device, m, n, k, variant):
     from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear_residual
 

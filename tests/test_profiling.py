@@ -31,6 +31,10 @@ def test_roles_of_current_kernel_templates():
     assert profiling.parse_kernel_name(BIG_LN_512) == (
         "linear_big_kernel", ["128", "512", "32", "2", "_Float16", "4", "_Float16"])
     assert [profiling.base_kernel_key(n) for n in (BIG_LN_512, BIG_QKV_256, FFN_ROLES)] == ["@ln", "qkv_proj", "ffn_ln"]
+    dma = ["_ZN3mpk17linear_dma_kernelILi0EDF16_EEvNS_10LinearArgsE", "_ZN3mpk17linear_dma_kernelILi1EDF16_EEvNS_10LinearArgsE",
+           "_ZN3mpk17linear_dma_kernelILi3EfEEvNS_10LinearArgsE"]
+    assert profiling.parse_kernel_name(dma[2]) == ("linear_dma_kernel", ["3", "float"])
+    assert [profiling.base_kernel_key(n) for n in dma] == ["qkv_proj", "ffn_in", "@residual"]
 
 
 def test_parse_mangled_and_demangled_names():

@@ -492,8 +492,14 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
 
   __shared__ _Float16 ks_lds[2][SH::KBUF];
   // V is staged row-major like K (one 16-byte store per chunk); the P V product
-  // reads its V^T fragments with LDS transpose loads (ds_read_b64_tr_b16)
-  constexpr int LDVR = SH::LDK;
+  // reads its V^T fragments with LDS transpose loads (ds_read_b64_tr_b16).  Each
+  // 32-lane half of such a read covers 4 consecutive keys x 64 bytes of head dims,
+  // which meet no bank conflict on gfx950 only when the row stride is an odd
+  // multiple of 64 bytes (measured with SQ_LDS_BANK_CONFLICT; the K tile's
+  // 16-byte-padded stride, right for the K fragment reads, conflicts two ways here):
+  // unpadded rows at hd 32.  (At hd 64 that takes 192-byte rows, which measured no
+  // faster than the K stride; hd 64 keeps it.)
+  constexpr int LDVR = HD == 32 ? HD : SH::LDK;
   __shared__ _Float16 vr_lds[2][KTILE * LDVR];
   __shared__ float kbias[2][KTILE];
 

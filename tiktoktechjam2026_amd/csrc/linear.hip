@@ -19,6 +19,7 @@
 // the LayerNorm epilogue a wave owns whole rows (BN == N), so the row
 // statistics need only two cross-lane shuffles.
 #include <algorithm>
+#include <type_traits>
 
 #include "mpk_common.h"
 
@@ -564,6 +565,277 @@ static hipError_t launch_linear_big(const LinearArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ---- LDS-DMA projection (FP16 X) ----
+// The same 256 x 256 output tiles, wave shapes, paired W-row mapping, MFMAs and
+// epilogues as linear_big_kernel<256, 256, ...>, with the operands staged
+// differently: X and W chunks 32 wide in K travel global -> LDS as LDS-DMA copies
+// (global_load_lds_dwordx4, no registers, no LDS store instructions), through a
+// ring of four LDS stages: while chunk q is multiplied, chunk q + 1 is read from
+// LDS into fragment registers and chunks q + 2 .. q + 4 are in flight.  Per chunk
+// each wave issues four 1-KB copies spread between its 32 MFMAs, waits for its own
+// copies of the chunk it is about to read, and meets the other waves at one
+// barrier, which also tells it that the stage it refills next has been read by
+// everyone.
+//
+// A staged row is 64 bytes (four 16-byte chunks of 8 k values) with no padding;
+// chunk c of row R sits in slot c ^ ((R / 2) % 4).  With that swizzle the
+// fragment reads (lane r of a 16-lane group reads row R0 + r at one chunk) count no
+// LDS bank conflicts on gfx950, where the plain layout, other XOR swizzles of the
+// row bits and even 80-byte padded rows count two-way conflicts (measured with
+// SQ_LDS_BANK_CONFLICT).
+//
+// Rows past M (or N) copy the last existing row (their products only reach output
+// rows or columns that are not stored), so every copy reads memory inside X and W.
+// Completion is tracked by count: after a wave issues a chunk's copies it issues
+// the next two chunks' copies and, when a tile ended in between, that tile's
+// output stores; s_waitcnt vmcnt(8 [+ stores]) before the chunk is read means
+// that its own copies have landed (vector-memory operations of a wave complete in issue
+// order).  Output stores therefore always issue the same number of instructions
+// per tile: columns past N go to an offset outside the tile's buffer resource
+// and rows past M lie outside it, and the hardware drops both.
+constexpr int kDmaMaxN = 8192;  // the bias row lives in LDS
+
+__device__ __forceinline__ int dma_swizzle(int r) { return (r >> 1) & 3; }
+
+template <int EPI, typename OT>
+__global__ __launch_bounds__(512) void linear_dma_kernel(LinearArgs a) {
+  constexpr int BM = 256, BN = 256, BK = 32, NS = 4;
+  constexpr int TM = 8, PN = 2;                         // 128 x 64 per wave, as linear_big_kernel
+  constexpr int XBYTES = BM * BK * 2;                   // X part of a stage
+  constexpr int SBYTES = (BM + BN) * BK * 2;            // one stage: 32 KB
+  constexpr int STORES = TM * PN * (sizeof(OT) == 4 ? 2 : 1);  // store instructions per wave and tile
+  static_assert(EPI == kEpiBias || EPI == kEpiBiasGelu || EPI == kEpiBiasResidual, "plain epilogues");
+  __shared__ __align__(16) unsigned char stages[NS * SBYTES];
+  __shared__ __align__(16) _Float16 bias_s[kDmaMaxN];
+
+  const _Float16* __restrict__ X = static_cast<const _Float16*>(a.x);
+  const _Float16* __restrict__ W = a.w;
+  const int64_t M = a.m;
+  const int N = a.n, K = a.k;
+  const int nbn = (N + BN - 1) / BN;
+  const int tiles = (int)((M + BM - 1) / BM) * nbn;
+  const int nk = K / BK;  // >= 4, checked by the launcher
+
+  // tile list as in linear_big_kernel: XCD x owns a contiguous share of the tiles
+  const int G = gridDim.x;
+  int tile, stride, last;
+  if ((G & 7) == 0) {
+    const int xcd = blockIdx.x & 7;
+    stride = G >> 3;
+    last = (int)((int64_t)tiles * (xcd + 1) / 8);
+    tile = (int)((int64_t)tiles * xcd / 8) + (blockIdx.x >> 3);
+  } else {
+    stride = G;
+    last = tiles;
+    tile = blockIdx.x;
+  }
+  if (tile >= last) return;  // uniform per workgroup, before any barrier
+  const int nq = ((last - tile + stride - 1) / stride) * nk;  // chunks this workgroup computes
+
+  const int l = threadIdx.x & 63, wave = wave_id();
+  const int r = l & 15, g = l >> 4;
+  const int wm = wave & 1, wn = wave >> 1;
+
+  for (int i = 8 * (int)threadIdx.x; i < N; i += 8 * 512)
+    *reinterpret_cast<h8*>(&bias_s[i]) = *reinterpret_cast<const h8*>(a.bias + i);
+
+  // ---- copies: wave w fills X rows and W slots 32 w .. 32 w + 31 of every stage ----
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)stages;
+  const int rr = l >> 2;                                // row within a 16-row copy block
+  const int cc = (l & 3) ^ dma_swizzle(rr);             // k chunk this lane copies
+  int xrow[2], wfeat[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    xrow[i] = 32 * wave + 16 * i + rr;
+    wfeat[i] = 32 * wave + 8 * (rr >> 2) + 4 * i + (rr & 3);  // LDS slot 32 w + 16 i + rr holds pair_row(rr, i)
+  }
+  uint32_t xoff[2], woff[2];
+  const _Float16* xsrc = X;
+  const _Float16* wsrc = W;
+  int ctile = tile, ckc = 0;  // next chunk to copy
+  auto copy_tile = [&](int t) {
+    const int64_t m0 = (int64_t)(t / nbn) * BM;
+    const int n0 = (t % nbn) * BN;
+    const int xmax = (int)min<int64_t>(BM, M - m0) - 1, wmax = min(BN, N - n0) - 1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      xoff[i] = (uint32_t)(min(xrow[i], xmax) * K + 8 * cc) * 2u;
+      woff[i] = (uint32_t)(min(wfeat[i], wmax) * K + 8 * cc) * 2u;
+    }
+    xsrc = X + m0 * K;
+    wsrc = W + (int64_t)n0 * K;
+  };
+  copy_tile(tile);
+  // copy j (0..3) of the current chunk into stage `st`
+  auto copy = [&](int j, int st) {
+    const uint32_t dst = lds0 + (uint32_t)(st * SBYTES + (j >> 1) * XBYTES + (2 * wave + (j & 1)) * 1024);
+    const _Float16* src = ((j >> 1) ? wsrc : xsrc) + ckc * BK;
+    dma16((j >> 1) ? woff[j & 1] : xoff[j & 1], src, dst);
+  };
+  // after the chunk's four copies: the next chunk; past the last one the copies
+  // repeat the last chunk into a stage nobody reads again
+  auto advance = [&]() {
+    if (ckc + 1 < nk) {
+      ++ckc;
+    } else if (ctile + stride < last) {
+      ckc = 0;
+      ctile += stride;
+      copy_tile(ctile);
+    }
+  };
+
+  f4 acc[PN][2][TM];
+#pragma unroll
+  for (int p = 0; p < PN; ++p)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int t = 0; t < TM; ++t) acc[p][tt][t] = zero4();
+
+  const uint32_t lane_off = (uint32_t)(r * 64 + ((g ^ dma_swizzle(r)) << 4));
+  OT* Y = static_cast<OT*>(a.y);  // may alias a.residual (in-place residual add)
+  auto epilogue = [&](int etile) {
+    const int64_t m0 = (int64_t)(etile / nbn) * BM;
+    const int n0 = (etile % nbn) * BN;
+    const uint32_t rows = (uint32_t)min<int64_t>(BM, M - m0);
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(Y + m0 * N, rows * (uint32_t)N * (uint32_t)sizeof(OT));
+    const __amdgpu_buffer_rsrc_t rres =
+        make_rsrc(EPI == kEpiBiasResidual ? (const void*)(a.residual + m0 * N) : (const void*)a.x,
+                  EPI == kEpiBiasResidual ? rows * (uint32_t)N * 4u : 0u);
+#pragma unroll
+    for (int p = 0; p < PN; ++p) {
+      const int n = n0 + wn * 64 + 32 * p + 8 * g;
+      const bool ok = n < N;
+      const h8 bh = *reinterpret_cast<const h8*>(&bias_s[ok ? n : 0]);
+#pragma unroll
+      for (int t = 0; t < TM; ++t) {
+        const int row = wm * 128 + 16 * t + r;
+        const uint32_t e = (uint32_t)(row * N + n);
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = acc[p][0][t][i] + (float)bh[i];
+          v[4 + i] = acc[p][1][t][i] + (float)bh[4 + i];
+        }
+        if constexpr (EPI == kEpiBiasGelu) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = gelu_erf(v[j]);
+        }
+        if constexpr (EPI == kEpiBiasResidual) {
+          typedef float v4 __attribute__((ext_vector_type(4)));
+          const uint32_t ro = ok ? e * 4u : 0x80000000u;
+          const v4 r0 = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(rres, ro, 0, 0));
+          const v4 r1 = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(rres, ro + 16u, 0, 0));
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            v[j] += r0[j];
+            v[4 + j] += r1[j];
+          }
+        }
+        buffer_store8(yr, ok ? e * (uint32_t)sizeof(OT) : 0x80000000u, v, Y);
+      }
+    }
+  };
+
+  // Fragments: the W fragments of the chunk being multiplied and of the next one
+  // (double-buffered), and the X fragments, each replaced by the next chunk's as soon
+  // as its four MFMAs have been issued.  So the LDS reads of chunk q + 1 run beside
+  // the MFMAs of chunk q.
+  h8 wa[2][PN][2], xb[TM];
+  auto read_w = [&](int q, h8 (&w)[PN][2]) {
+    const unsigned char* sp = stages + (q & 3) * SBYTES + XBYTES;
+#pragma unroll
+    for (int p = 0; p < PN; ++p)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+        w[p][tt] = *reinterpret_cast<const h8*>(sp + (wn * 64 + 32 * p + 16 * tt) * 64 + lane_off);
+  };
+  auto read_x = [&](int q, int t) {
+    return *reinterpret_cast<const h8*>(stages + (q & 3) * SBYTES + (wm * 128 + 16 * t) * 64 + lane_off);
+  };
+
+  // prologue: chunks 0 .. 3 into stages 0 .. 3, chunk 0's fragments
+#pragma unroll
+  for (int q = 0; q < NS; ++q) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) copy(j, q);
+    advance();
+  }
+  wait_copies<12>();
+  lds_barrier();
+  read_w(0, wa[0]);
+#pragma unroll
+  for (int t = 0; t < TM; ++t) xb[t] = read_x(0, t);
+
+  int etile = tile, ekc = 0;  // chunk being multiplied
+  auto step = [&](int q, h8 (&wc)[PN][2], h8 (&wnx)[PN][2]) {
+    // this wave's copies of chunk q + 1 have landed (issued after them: chunks q + 2
+    // and q + 3, and within the first three chunks of a tile after the first, the
+    // previous tile's stores), and its fragment reads of chunk q are complete; after
+    // the barrier the same holds for every wave, so chunk q's stage is free for
+    // chunk q + 4
+    if (q >= nk && ekc < 3)
+      wait_copies<8 + STORES>();
+    else
+      wait_copies<8>();
+    lds_barrier();
+    read_w(q + 1, wnx);
+    const int nst = q & 3;
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+#pragma unroll
+      for (int p = 0; p < PN; ++p)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) acc[p][tt][t] = mfma32(wc[p][tt], xb[t], acc[p][tt][t]);
+      __builtin_amdgcn_sched_barrier(0);
+      xb[t] = read_x(q + 1, t);
+      if ((t & 1) == 0) copy(t >> 1, nst);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    advance();
+    if (ekc == nk - 1) {
+      epilogue(etile);
+#pragma unroll
+      for (int p = 0; p < PN; ++p)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int t = 0; t < TM; ++t) acc[p][tt][t] = zero4();
+      ekc = 0;
+      etile += stride;
+    } else {
+      ++ekc;
+    }
+  };
+  // the last step reads the fragments of a chunk past the end: a stage that the
+  // surplus copies have filled, read and never used
+  for (int q = 0; q < nq; q += 2) {
+    step(q, wa[0], wa[1]);
+    if (q + 1 >= nq) break;
+    step(q + 1, wa[1], wa[0]);
+  }
+  wait_copies<0>();  // no copy may land in LDS after the workgroup has left it
+}
+
+// Variant 8: FP16 X with K % 32 == 0, K >= 128 and N <= kDmaMaxN runs linear_dma_kernel;
+// other inputs run variant 7's kernel.
+template <typename XT, int EPI, typename OT>
+static hipError_t launch_linear_dma(const LinearArgs& a, hipStream_t s) {
+  constexpr bool kHalfX = std::is_same<XT, _Float16>::value;
+  if constexpr (kHalfX) {
+    if (a.k % 32 == 0 && a.k >= 128 && a.k <= (1 << 20) && a.n <= kDmaMaxN) {
+      const int64_t tiles = ((a.m + 255) / 256) * ((a.n + 255) / 256);
+      if (tiles > 0x7fffffff) return hipErrorInvalidConfiguration;
+      auto kernel = linear_dma_kernel<EPI, OT>;
+      int64_t grid = std::min<int64_t>(tiles, resident_grid(kernel, 512, 0));
+      if (grid >= 8) grid &= ~int64_t{7};
+      hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(512), 0, s, a);
+      return hipGetLastError();
+    }
+  }
+  return launch_linear_big<256, 256, 64, 2, XT, EPI, OT>(a, s);
+}
+
 template <int BM, int BN, int KC, int WAVES_M, typename XT, int EPI, typename OT>
 static hipError_t launch_linear(const LinearArgs& a, hipStream_t s) {
   const int64_t mb = (a.m + BM - 1) / BM;
@@ -582,6 +854,7 @@ static hipError_t launch_linear(const LinearArgs& a, hipStream_t s) {
 //   5: BM256 BN128 (2x2 waves, 128x64 per wave, double-buffered LDS)   large M and N
 //   6: as 5 with single-buffered LDS (two workgroups per CU)
 //   7: BM256 BN256 (2x4 waves, 128x64 per wave, double-buffered LDS)
+//   8: as 7 with LDS-DMA operand staging (FP16 X; other inputs run 7)
 template <typename XT, int EPI, typename OT>
 static hipError_t linear_variant(int variant, const LinearArgs& a, hipStream_t s) {
   switch (variant) {
@@ -592,6 +865,7 @@ static hipError_t linear_variant(int variant, const LinearArgs& a, hipStream_t s
     case 5: return launch_linear_big<256, 128, 64, 2, XT, EPI, OT>(a, s);
     case 6: return launch_linear_big<256, 128, 64, 1, XT, EPI, OT>(a, s);
     case 7: return launch_linear_big<256, 256, 64, 2, XT, EPI, OT>(a, s);
+    case 8: return launch_linear_dma<XT, EPI, OT>(a, s);
     default: return (hipError_t)MPK_EUNSUPPORTED;
   }
 }
@@ -633,7 +907,7 @@ using namespace mpk;
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 extern "C" int mpk_linear_auto_variant(int64_t m, int32_t n, int32_t k) {
-  if (n % 256 == 0 && k >= 256 && k <= (1 << 20) && ((m + 255) / 256) * (n / 256) >= 256) return 7;
+  if (n % 256 == 0 && k >= 256 && k <= (1 << 20) && ((m + 255) / 256) * (n / 256) >= 256) return 8;
   if (n % 128 == 0 && m >= 128 * 256) return 1;
   if (n % 128 == 0) return 4;
   if (n % 64 == 0) return 2;

@@ -235,6 +235,37 @@ __device__ __forceinline__ float max_over_groups(float v) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// ---- LDS-DMA copies (global -> LDS without registers) ----
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One 16-byte-per-lane LDS-DMA copy: lane l's 16 bytes at base + voff (base
+// wave-uniform, voff per lane) land at LDS byte address lds_base + 16 l
+// (lds_base wave-uniform, in M0).  Issued as inline assembly: the compiler does
+// not track it, so it neither counts it in its own vmcnt waits nor drains every
+// LDS read behind it (it cannot tell the copy's target buffer from the ones being
+// read).  Its completion is awaited explicitly with wait_copies.
+__device__ __forceinline__ void dma16(uint32_t voff, const void* base, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "s"(lds_base));
+}
+
+// Wait until at most N of this wave's vector-memory operations are outstanding
+// (they complete in issue order), and for all of its LDS operations.  gfx9
+// s_waitcnt encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14.
+template <int N>
+__device__ __forceinline__ void wait_copies() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier after wait_copies (which has also drained this wave's LDS
+// reads).  __syncthreads() would add a release fence, which waits for every
+// outstanding load and LDS-DMA copy - including the chunk copies meant to stay in
+// flight across it; the acquire fence keeps later LDS reads below the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Map a linear workgroup id so that consecutive tile indices land on the same
 // XCD (workgroups are dispatched round-robin over the 8 XCDs, each with its own
 // L2).  Identity when the grid is not a multiple of 8.

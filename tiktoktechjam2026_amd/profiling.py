@@ -345,6 +345,10 @@ def base_kernel_key(name: str) -> str:
         index = types[0] + 1 if types else -1
         epi = int(args[index]) if 0 <= index < len(args) and args[index].lstrip("-").isdigit() else -1
         return {0: "qkv_proj", 1: "ffn_in", 2: "@ln", 3: "@residual", 4: "@ln"}.get(epi, "linear")
+    if base == "linear_dma_kernel":
+        # linear_dma_kernel<EPI, OT>: the epilogue is the first template argument
+        epi = int(args[0]) if args and args[0].lstrip("-").isdigit() else -1
+        return {0: "qkv_proj", 1: "ffn_in", 3: "@residual"}.get(epi, "linear")
     if base in ("ffn_ln_kernel", "ffn_wide_kernel", "ffn_roles_kernel"):
         return "ffn_ln"
     if base == "residual_layernorm_kernel":
