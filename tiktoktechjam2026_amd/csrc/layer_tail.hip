@@ -65,10 +65,16 @@ constexpr int kLdsBudget = 160 * 1024;
 enum QkvMode : int { kQkvLds = 1, kQkvReg = 2 };
 
 // W: waves per workgroup (8, or 4 where 8-wave tiles would leave CUs idle).
+// Row strides: 16x16x32 fragment reads (lane r of a 16-lane group reads row R0 + r, the
+// four groups four consecutive 16-byte chunks) count no LDS bank conflicts on gfx950 when
+// the stride is an odd multiple of 32 bytes, and two-way conflicts when it is an odd
+// multiple of 16 bytes (measured with SQ_LDS_BANK_CONFLICT).  D + 16 and F + 16 halves are
+// odd multiples of 32 bytes for every supported width (multiples of 32).  Weight rows are
+// stored at LDS row w_slot(row), so the 16 rows of a fragment are consecutive.
 template <int D, int F, int TM, bool STAGE1, bool QKV, int QMODE, int W>
 struct TailShape {
-  static constexpr int LDD = D + 8;  // row stride of [*, D] tiles (halves)
-  static constexpr int LDF = F + 8;  // row stride of Wout [D, F] (halves)
+  static constexpr int LDD = D + 16;  // row stride of [*, D] tiles (halves)
+  static constexpr int LDF = F + 16;  // row stride of Wout [D, F] (halves)
   static constexpr int WO = 0;
   static constexpr int WIN = WO + (STAGE1 ? D * LDD : 0);
   static constexpr int WOUT = WIN + (STAGE1 ? F * LDD : 0);
@@ -91,11 +97,12 @@ struct TailShape {
   static constexpr int BYTES = PARAM_OFF * 2 + NPARAM * 4;
 };
 
-// Two-phase staging of a [ROWS, COLS] FP16 matrix into LDS (row stride LD): load()
-// issues all of this thread's global reads, store() writes them to LDS, so the
-// reads of every staged array can be in flight together.
+// Two-phase staging of a [ROWS, COLS] FP16 matrix into LDS (row stride LD, row j at
+// LDS row w_slot(j)): load() issues all of this thread's global reads, store() writes
+// them to LDS, so the reads of every staged array can be in flight together.
 template <int ROWS, int COLS, int LD, bool ON, int NT>
 struct MatStage {
+  static_assert(!ON || ROWS % 32 == 0, "w_slot permutes rows within groups of 32");
   static constexpr int CPR = COLS / 8;
   static constexpr int CHUNKS = ON ? ROWS * CPR : 0;
   static constexpr int PER = ON ? (CHUNKS + NT - 1) / NT : 1;
@@ -114,7 +121,7 @@ struct MatStage {
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int c = threadIdx.x + i * NT;
-        if (c < CHUNKS) *reinterpret_cast<h8*>(&dst[(c / CPR) * LD + (c % CPR) * 8]) = v[i];
+        if (c < CHUNKS) *reinterpret_cast<h8*>(&dst[w_slot(c / CPR) * LD + (c % CPR) * 8]) = v[i];
       }
     }
   }
@@ -310,7 +317,7 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
               w[p][tt] = *reinterpret_cast<const h8*>(
-                  &lds[SH::WO + (32 * p + pair_row(r, tt)) * SH::LDD + ks * 32 + 8 * g]);
+                  &lds[SH::WO + (32 * p + 16 * tt + r) * SH::LDD + ks * 32 + 8 * g]);
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int p = 0; p < PN; ++p)
@@ -362,7 +369,7 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
             wi[ks][tt] = *reinterpret_cast<const h8*>(
-                &lds[SH::WIN + (32 * fq + pair_row(r, tt)) * SH::LDD + ks * 32 + 8 * g]);
+                &lds[SH::WIN + (32 * fq + 16 * tt + r) * SH::LDD + ks * 32 + 8 * g]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
@@ -386,7 +393,7 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
             wo[p][tt] = *reinterpret_cast<const h8*>(
-                &lds[SH::WOUT + (32 * p + pair_row(r, tt)) * SH::LDF + 32 * fq + 8 * g]);
+                &lds[SH::WOUT + (32 * p + 16 * tt + r) * SH::LDF + 32 * fq + 8 * g]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int p = 0; p < PN; ++p)
@@ -471,7 +478,7 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt) {
             const h8 w = *reinterpret_cast<const h8*>(
-                &lds[SH::WQKV + (32 * op + pair_row(r, tt)) * SH::LDD + ks * 32 + 8 * g]);
+                &lds[SH::WQKV + (32 * op + 16 * tt + r) * SH::LDD + ks * 32 + 8 * g]);
 #pragma unroll
             for (int t = 0; t < TM; ++t) qacc[t][tt] = mfma32(w, n1f[t][ks], qacc[t][tt]);
           }

@@ -209,13 +209,6 @@ __global__ __launch_bounds__(kBlock) void linear_kernel(LinearArgs a) {
 }
 
 
-// LDS slot of weight row j: within each 32-row group, row pair_row(r, tt) goes
-// to slot 16 tt + r, so the 16 lanes of one fragment read consecutive padded
-// rows (no bank conflicts) instead of pair_row's strided set.
-__device__ __forceinline__ int w_slot(int j) {
-  return (j & ~31) | (((j >> 2) & 1) << 4) | ((j >> 3) & 3) << 2 | (j & 3);
-}
-
 // Large-tile projection for wide models: a BM (tokens) x BN (features) output
 // tile per workgroup of BM/128 x BN/64 waves, each wave 128 x 64 (8 token tiles x
 // 2 feature pairs).  K is staged in BK-wide chunks (64, or 32 where a wide tile

@@ -50,6 +50,13 @@ __device__ __forceinline__ f4 mfma16(const h4& a, const h4& b, const f4& c) {
 
 __device__ __forceinline__ int pair_row(int q, int t) { return 8 * (q >> 2) + 4 * t + (q & 3); }
 
+// LDS slot of weight row j: within each 32-row group, row pair_row(r, tt) goes
+// to slot 16 tt + r, so the 16 lanes of one fragment read consecutive padded
+// rows (no bank conflicts) instead of pair_row's strided set.
+__device__ __forceinline__ int w_slot(int j) {
+  return (j & ~31) | (((j >> 2) & 1) << 4) | ((j >> 3) & 3) << 2 | (j & 3);
+}
+
 // ---- 32x32x16 products ----
 // Operand layouts of v_mfma_f32_32x32x16_f16 (lane l, i = l % 32, h = l / 32):
 //   A (32 x 16): row i, k = 8h .. 8h+7     B (16 x 32): column i, k = 8h .. 8h+7
