@@ -683,7 +683,13 @@ __global__ __launch_bounds__(kRT) void ffn_roles_kernel(FfnArgs a) {
     for (int i = 0; i < N; ++i) yacc[i >> 1] = mfma32x32(fr[i], (i & 1) ? hb1 : hb0, yacc[i >> 1]);
   };
 
-  // tile epilogue: + b_out + residual, two-pass LayerNorm over the row, stores
+  // tile epilogue: + b_out + residual, two-pass LayerNorm over the row, stores.
+  // vmcnt counts loads and stores in one in-order counter, so a residual load
+  // issued after a store waits for that store too: every residual load is issued
+  // before the first store (RUNS_IN_FLIGHT runs of 8 features at a time), and the
+  // stores then drain while the next tile runs.  Offsets are a per-lane base plus
+  // immediates (the base is laundered so that the compiler does not hoist 32
+  // precomputed offsets into registers).
   auto epilogue = [&](int64_t t) {
     const int64_t row0 = t * kTok + 32 * sl;
     const uint32_t rows = (uint32_t)max<int64_t>(0, min<int64_t>(32, M - row0));
@@ -695,25 +701,41 @@ __global__ __launch_bounds__(kRT) void ffn_roles_kernel(FfnArgs a) {
     const float* gm = prm + D;
     const float* bt = prm + 2 * D;
     typedef float v4 __attribute__((ext_vector_type(4)));
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    constexpr int RUNS = 2 * PT;            // runs of 8 features: run i = (p, r) = (i / 2, i % 2)
+    constexpr int RUNS_IN_FLIGHT = 8;
+    uint32_t base4 = (uint32_t)((li * D + 8 * hh) * 4);
+    uint32_t base_o = (uint32_t)((li * D + 8 * hh) * sizeof(OT));
+    asm volatile("" : "+v"(base4), "+v"(base_o));
+    v4 rv[RUNS_IN_FLIGHT][2];
+    auto load_run = [&](int i) {
+      const uint32_t off = base4 + (uint32_t)((32 * (i >> 1) + 16 * (i & 1)) * 4);
+      rv[i % RUNS_IN_FLIGHT][0] = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, 0));
+      rv[i % RUNS_IN_FLIGHT][1] = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(rr, off + 16, 0, 0));
+    };
+#pragma unroll
+    for (int i = 0; i < RUNS_IN_FLIGHT; ++i) load_run(i);
     float sum = 0.f;
 #pragma unroll
-    for (int p = 0; p < PT; ++p)
+    for (int i = 0; i < RUNS; ++i) {
+      const int p = i >> 1, r = i & 1, n = 32 * p + 16 * r + 8 * hh;
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int n = 32 * p + 16 * r + 8 * hh;
-        const uint32_t off = (uint32_t)((li * D + n) * 4);
-        const v4 r0 = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, 0));
-        const v4 r1 = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(rr, off + 16, 0, 0));
-        float vv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float v = (yacc[p][8 * r + j] + bo[n + j]) + (j < 4 ? r0[j] : r1[j - 4]);
-          yacc[p][8 * r + j] = v;
-          vv[j] = v;
-          sum += v;
-        }
-        buffer_store8(ro, off, vv, a.residual_out);
+      for (int j = 0; j < 8; ++j) {
+        const float v = (yacc[p][8 * r + j] + bo[n + j]) + rv[i % RUNS_IN_FLIGHT][j >> 2][j & 3];
+        yacc[p][8 * r + j] = v;
+        sum += v;
       }
+      if (i + RUNS_IN_FLIGHT < RUNS) load_run(i + RUNS_IN_FLIGHT);
+    }
+#pragma unroll
+    for (int i = 0; i < RUNS; ++i) {
+      const int p = i >> 1, r = i & 1;
+      const uint32_t off = base4 + (uint32_t)((32 * p + 16 * r) * 4);
+      const v4 v0 = {yacc[p][8 * r + 0], yacc[p][8 * r + 1], yacc[p][8 * r + 2], yacc[p][8 * r + 3]};
+      const v4 v1 = {yacc[p][8 * r + 4], yacc[p][8 * r + 5], yacc[p][8 * r + 6], yacc[p][8 * r + 7]};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v0), ro, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v1), ro, off + 16, 0, 0);
+    }
     const float inv_d = 1.0f / (float)D;
     const float mean = sum_over_halves(sum) * inv_d;
     float sq = 0.f;
@@ -733,7 +755,7 @@ __global__ __launch_bounds__(kRT) void ffn_roles_kernel(FfnArgs a) {
         float o[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = (yacc[p][8 * r + j] - mean) * rstd * gm[n + j] + bt[n + j];
-        buffer_store8(no, (uint32_t)((li * D + n) * sizeof(OT)), o, static_cast<OT*>(a.normalized_out));
+        buffer_store8(no, base_o + (uint32_t)((32 * p + 16 * r) * sizeof(OT)), o, static_cast<OT*>(a.normalized_out));
       }
 #pragma unroll
     for (int p = 0; p < PT; ++p)
