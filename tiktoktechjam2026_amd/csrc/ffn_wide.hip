@@ -768,9 +768,24 @@ __global__ __launch_bounds__(kRT) void ffn_roles_kernel(FfnArgs a) {
   lds_barrier();
   int b3 = 0, c2 = 0;   // (g - 2) % 3 and the chunk of position g - 2
   int64_t t2 = 0;       // tile of position g - 2
+  // Residual prefetch: over the PF_STEPS steps before a tile's last one, each matrix
+  // wave copies its 32 token rows of the residual (1 KB each, one LDS-DMA copy per
+  // row) into the slack LDS area, whose contents nobody reads: the rows are then in
+  // the L2 when the epilogue loads them, and the HBM reads of every workgroup's
+  // epilogue are spread over those steps instead of arriving at once.  The copies
+  // are older than every load the compiler counts, so its vmcnt waits stay exact.
+  constexpr int PF_STEPS = 8, PF_ROWS = 32 / PF_STEPS;
+  const uint32_t pf_lane = ((uint32_t)l * 16u) % (uint32_t)(D * 4);  // inside the row for any D
+  const uint32_t pf_sink = (uint32_t)(uintptr_t)(lds_void*)slack;
 #pragma unroll 1
   for (int g = 2; g < G + 2; ++g) {
     s2(b3, g & 1);
+    if (c2 >= C - 1 - PF_STEPS && c2 < C - 1) {
+      const int64_t r0 = (tile0 + t2 * gridDim.x) * kTok + 32 * sl + PF_ROWS * (c2 - (C - 1 - PF_STEPS));
+#pragma unroll
+      for (int i = 0; i < PF_ROWS; ++i)
+        if (r0 + i < M) dma16(pf_lane, a.residual + (r0 + i) * D, pf_sink);
+    }
     // the operand reads are done before the barrier: the next step's copies reuse
     // this W_out buffer
     __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
