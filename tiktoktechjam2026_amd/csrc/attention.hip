@@ -34,6 +34,7 @@ namespace mpk {
 
 // The running max (log2 units) is raised only when a tile exceeds it by more than this.
 constexpr float kRescaleLog2 = 8.0f;
+constexpr float kRescaleWeight = 256.0f;  // 2^kRescaleLog2: a weight 2^(s*c - m) above it calls for a raise
 
 struct AttnArgs {
   const void* q;
@@ -570,6 +571,10 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
   // ---- register prefetch / LDS staging of one K/V tile (both row-major) ----
   h8 kreg[SH::PER_THREAD], vreg[SH::PER_THREAD];
   float breg = 0.f;
+  // Key bias (-inf for masked keys and keys past the sequence end): staged only for
+  // tiles that read it, which is every tile with a key mask and otherwise only a tile
+  // that runs past the sequence end (wave-uniform).
+  bool bias_staged = false;
   const uint32_t krow_bytes = (uint32_t)(a.ks[2] * (int64_t)sizeof(IT));
   const uint32_t vrow_bytes = (uint32_t)(a.vs[2] * (int64_t)sizeof(IT));
   auto fetch = [&](int kb) {
@@ -588,7 +593,8 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
       const int key = cc / SH::CPK, col = (cc % SH::CPK) * 8;
       if (cc < SH::CHUNKS) vreg[i] = buffer_load8_as_half(vr, key * vrow_bytes + col * (uint32_t)sizeof(IT), Vp);
     }
-    if (threadIdx.x < KTILE) {
+    bias_staged = KEYMASK || kb + KTILE > S;
+    if (bias_staged && threadIdx.x < KTILE) {
       const int gk = kb + threadIdx.x;
       bool valid = gk < S;
       if (KEYMASK && valid) valid = kv_valid[gk] != 0;
@@ -605,7 +611,7 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
         *reinterpret_cast<h8*>(&vr_lds[buf][key * LDVR + col]) = vreg[i];
       }
     }
-    if (threadIdx.x < KTILE) kbias[buf][threadIdx.x] = breg;
+    if (bias_staged && threadIdx.x < KTILE) kbias[buf][threadIdx.x] = breg;
   };
   // V^T fragment (A operand of O^T = V^T P^T) from the row-major V tile: MFMA row i
   // (head dim 32 dt + kappa(i)) and keys k0 .. k0 + 7, as two transpose loads.  Within
@@ -686,44 +692,47 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
       }
     }
 
-    // online softmax with a lazily raised max (see attention_kernel); the
-    // lane-local max over the tile decides whether the row-wide one is needed at all
-    float mx = sc[0][0];
+    // online softmax with a lazily raised max (see attention_kernel): the row max
+    // is raised only when a score exceeds it by more than kRescaleLog2.
+    // raise_max: the lane-local max over the tile decides whether the row-wide one
+    // is needed at all; if so the row max is raised and O and l are rescaled.
+    auto raise_max = [&]() {
+      float mx = sc[0][0];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      if (EDGE && nb >= nbv) break;
+      for (int nb = 0; nb < NB; ++nb) {
+        if (EDGE && nb >= nbv) break;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[nb][e]);
-    }
-    const float ms = mx * c;  // this lane's max of s*c
-    const bool want = (MAYBE_FRESH && fresh) || ms - mrow > kRescaleLog2;
-    if (__builtin_amdgcn_ballot_w64(want)) {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ms), __float_as_uint(ms), false, false);
-      const float full = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-      const bool is_fresh = MAYBE_FRESH && fresh;
-      const bool shift_row = is_fresh ? (full > -INFINITY) : (full - mrow > kRescaleLog2);
-      float alpha = 1.f;
-      if (shift_row) {
-        if (!is_fresh) alpha = __builtin_amdgcn_exp2f(mrow - full);
-        mrow = full;
-        fresh = false;
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[nb][e]);
       }
+      const float ms = mx * c;  // this lane's max of s*c
+      const bool want = (MAYBE_FRESH && fresh) || ms - mrow > kRescaleLog2;
+      if (__builtin_amdgcn_ballot_w64(want)) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ms), __float_as_uint(ms), false, false);
+        const float full = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        const bool is_fresh = MAYBE_FRESH && fresh;
+        const bool shift_row = is_fresh ? (full > -INFINITY) : (full - mrow > kRescaleLog2);
+        float alpha = 1.f;
+        if (shift_row) {
+          if (!is_fresh) alpha = __builtin_amdgcn_exp2f(mrow - full);
+          mrow = full;
+          fresh = false;
+        }
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
-      // the row sums of queries (l % 16) and (l % 16) + 16 live in lanes 0..15
-      const float a0 = __shfl(alpha, l & 15), a1 = __shfl(alpha, (l & 15) + 16);
-      lsum[0] *= a0;
-      lsum[1] *= a1;
-    }
-    const float negm = -mrow;
-
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      if (EDGE && nb >= nbv) break;
-      // p = 2^(s c - m) rounded to FP16: the two 16-key B fragments
-      h8 pf[2];
+        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+        // the row sums of queries (l % 16) and (l % 16) + 16 live in lanes 0..15
+        const float a0 = __shfl(alpha, l & 15), a1 = __shfl(alpha, (l & 15) + 16);
+        lsum[0] *= a0;
+        lsum[1] *= a1;
+      }
+    };
+    // p = 2^(s c - m) rounded to FP16 for block nb: the two 16-key B fragments
+    auto weights = [&](int nb, h8 (&pf)[2]) {
+      const float negm = -mrow;
 #pragma unroll
       for (int e = 0; e < 16; ++e) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(fmaf(sc[nb][e], c, negm));
+    };
+    // l += the FP16 weights; O^T += V^T P^T
+    auto accumulate = [&](int nb, const h8 (&pf)[2]) {
       lsum = mfma32(ones, pf[0], lsum);
       lsum = mfma32(ones, pf[1], lsum);
 #pragma unroll
@@ -733,6 +742,95 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
           const h8 va = vt_frag(vtb, dt, 32 * nb + 16 * s2 + 8 * hf);
           oacc[dt] = mfma32x32(va, pf[s2], oacc[dt]);
         }
+    };
+
+    // (head dim 32 with 64-key tiles only: the tile's weights held at once cost a
+    // wave per SIMD of occupancy at head dim 64 and with 128-key tiles)
+    if constexpr (!EDGE && !MAYBE_FRESH && HD == 32 && KTILE == 64) {
+      // Steady tiles: the weights are computed from the current row max first, and
+      // the rescale test runs on them - a weight above 2^kRescaleLog2 means a score
+      // above the max by more than kRescaleLog2 (an overflowing weight is +inf,
+      // which counts too) - as 3-input packed FP16 maxima over the weight registers,
+      // NB * 4 instructions instead of the 16 NB FP32 ones over the scores.  Only
+      // when it fires (rarely once a row has seen its first keys) are the scores
+      // computed again (the K tile is still in LDS; keeping them would cost the
+      // registers of a wave per SIMD), the score-based test above run and the
+      // weights recomputed.
+      h8 pf[NB][2];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) weights(nb, pf[nb]);
+      typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+      auto pair = [&](int k) {  // packed weight pair k of the tile (NB * 8 pairs, one register each)
+        const h8 v = pf[k >> 3][(k >> 2) & 1];
+        const int w = 2 * (k & 3);
+        return h2v{v[w], v[w + 1]};
+      };
+      h2v pm = __builtin_elementwise_maximum(pair(0), pair(1));
+#pragma unroll
+      for (int k = 2; k < NB * 8; k += 2)
+        pm = __builtin_elementwise_maximum(__builtin_elementwise_maximum(pm, pair(k)), pair(k + 1));
+      const float pmax = fmaxf((float)pm[0], (float)pm[1]);
+      if (__builtin_amdgcn_ballot_w64(!(pmax <= kRescaleWeight))) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          sc[nb] = f16v{};
+#pragma unroll
+          for (int st = 0; st < QS; ++st) {
+            const h8 ka = *reinterpret_cast<const h8*>(&ksb[(32 * nb + trow) * SH::LDK + 16 * st + 8 * hf]);
+            sc[nb] = mfma32x32(ka, qf[st], sc[nb]);
+          }
+        }
+        raise_max();
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) weights(nb, pf[nb]);
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) accumulate(nb, pf[nb]);
+    } else {
+      // the score-based test, then each block's weights, row sums and P V
+      float mx = sc[0][0];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        if (EDGE && nb >= nbv) break;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[nb][e]);
+      }
+      const float ms = mx * c;  // this lane's max of s*c
+      const bool want = (MAYBE_FRESH && fresh) || ms - mrow > kRescaleLog2;
+      if (__builtin_amdgcn_ballot_w64(want)) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ms), __float_as_uint(ms), false, false);
+        const float full = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        const bool is_fresh = MAYBE_FRESH && fresh;
+        const bool shift_row = is_fresh ? (full > -INFINITY) : (full - mrow > kRescaleLog2);
+        float alpha = 1.f;
+        if (shift_row) {
+          if (!is_fresh) alpha = __builtin_amdgcn_exp2f(mrow - full);
+          mrow = full;
+          fresh = false;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+        const float a0 = __shfl(alpha, l & 15), a1 = __shfl(alpha, (l & 15) + 16);
+        lsum[0] *= a0;
+        lsum[1] *= a1;
+      }
+      const float negm = -mrow;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        if (EDGE && nb >= nbv) break;
+        h8 pf[2];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(fmaf(sc[nb][e], c, negm));
+        lsum = mfma32(ones, pf[0], lsum);
+        lsum = mfma32(ones, pf[1], lsum);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            const h8 va = vt_frag(vtb, dt, 32 * nb + 16 * s2 + 8 * hf);
+            oacc[dt] = mfma32x32(va, pf[s2], oacc[dt]);
+          }
+      }
     }
   };
 
@@ -742,8 +840,10 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
   // of every wave and run the check-free steady-state body in a loop of their
   // own; the split point is workgroup-uniform, so every wave meets the same
   // barriers.
-  auto step = [&](int tile, auto first_tag, auto edge_tag) {
-    const int cur = tile & 1;
+  // At head dim 32 the steady-state loop runs two tiles per iteration with
+  // compile-time buffer indices (odd tile: buffer 1, even tile: buffer 0), so its
+  // LDS addresses are a per-lane base plus immediates.
+  auto step_in = [&](int tile, int cur, auto first_tag, auto edge_tag) {
     const int kb = tile * KTILE;
     const bool more = tile + 1 < ntiles;
     if (more) fetch(kb + KTILE);
@@ -751,14 +851,25 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
     if (more) stash(cur ^ 1);
     __syncthreads();
   };
+  auto step = [&](int tile, auto first_tag, auto edge_tag) { step_in(tile, tile & 1, first_tag, edge_tag); };
   const int steady_end = KEYMASK ? 1 : max(1, min(ntiles, (a.causal ? min(q0, S) : S) / KTILE));
 
   fetch(0);
   stash(0);
   __syncthreads();
   step(0, std::true_type{}, std::true_type{});
-  for (int tile = 1; tile < steady_end; ++tile) step(tile, std::false_type{}, std::false_type{});
-  for (int tile = steady_end; tile < ntiles; ++tile) step(tile, std::false_type{}, std::true_type{});
+  int tile = 1;
+  if constexpr (HD == 32 && KTILE == 64) {
+    for (; tile + 1 < steady_end; tile += 2) {
+      step_in(tile, 1, std::false_type{}, std::false_type{});
+      step_in(tile + 1, 0, std::false_type{}, std::false_type{});
+    }
+    if (tile < steady_end) step_in(tile++, 1, std::false_type{}, std::false_type{});
+  } else {
+    // (unrolled, head dim 64 needs two registers more than four waves per SIMD allow)
+    for (; tile < steady_end; ++tile) step(tile, std::false_type{}, std::false_type{});
+  }
+  for (; tile < ntiles; ++tile) step(tile, std::false_type{}, std::true_type{});
 
   // ---- normalise and store: lane (i, hf) holds head dims 32 dt + 16 s + 8 hf + j in register 8 s + j ----
   const float a0 = __shfl(lsum[0], qi & 15), a1 = __shfl(lsum[1], qi & 15);
