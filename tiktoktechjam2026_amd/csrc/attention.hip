@@ -481,7 +481,8 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 // A operand (rows 0 and 1 pick the queries i and i + 16 out of the P fragment
 // layout), so l sums exactly the FP16 weights that multiply V.
 template <int HD, int NW, int KTILE, typename IT, typename OT, bool KEYMASK>
-__global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD == 32 && KTILE == 64 ? 4 : 1)))
+void attention32_kernel(AttnArgs a) {
   constexpr int NT = 64 * NW;
   using SH = AttnShape<HD, KTILE, NT>;
   constexpr int QB = 32 * NW;     // queries per workgroup, 32 per wave
@@ -756,6 +757,10 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
       // computed again (the K tile is still in LDS; keeping them would cost the
       // registers of a wave per SIMD), the score-based test above run and the
       // weights recomputed.
+      static_assert(DT == 1, "one 32-row head-dim tile");
+      // The first block's V^T fragments are read before the test: its branch would
+      // keep them below it, with their LDS latency in front of the first P V MFMA.
+      const h8 va0[2] = {vt_frag(vtb, 0, 8 * hf), vt_frag(vtb, 0, 16 + 8 * hf)};
       h8 pf[NB][2];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) weights(nb, pf[nb]);
@@ -784,8 +789,12 @@ __global__ __launch_bounds__(64 * NW) void attention32_kernel(AttnArgs a) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) weights(nb, pf[nb]);
       }
+      lsum = mfma32(ones, pf[0][0], lsum);
+      lsum = mfma32(ones, pf[0][1], lsum);
+      oacc[0] = mfma32x32(va0[0], pf[0][0], oacc[0]);
+      oacc[0] = mfma32x32(va0[1], pf[0][1], oacc[0]);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) accumulate(nb, pf[nb]);
+      for (int nb = 1; nb < NB; ++nb) accumulate(nb, pf[nb]);
     } else {
       // the score-based test, then each block's weights, row sums and P V
       float mx = sc[0][0];
