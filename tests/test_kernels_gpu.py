@@ -128,6 +128,23 @@ def test_mixed_linear(hip_device, m, n, k, variant):
                 _close(y, ref, tol, tol, f"linear in={in_dtype} out={out_dtype} gelu={gelu}")
 
 
+@pytest.mark.parametrize(
+    "m,n,k", [(8192, 384, 128), (333, 2048, 512), (1000, 200, 192), (130, 768, 256), (70000, 768, 256)]
+)
+def test_linear_large_tile_variants_bit_identical(hip_device, m, n, k):
+    """Variants 7 (register staging) and 8 (LDS-DMA staging) accumulate the same MFMAs
+    in the same order: identical outputs, including ragged tiles in M and N."""
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear
+
+    print(f"\n[linear 7/8] m={m} n={n} k={k}", flush=True)
+    lin = _linear(k, n, hip_device, 29)
+    x = _randn((m, k), 31).to(hip_device, torch.float16)
+    for out_dtype in (torch.float32, torch.float16):
+        for gelu in (False, True):
+            y7, y8 = (mixed_linear(x, lin, output_dtype=out_dtype, fuse_gelu=gelu, variant=v) for v in (7, 8))
+            assert torch.equal(y7, y8), f"out={out_dtype} gelu={gelu}"
+
+
 @pytest.mark.parametrize("n,variant", [(8, 0), (256, 7), (128, 1)])
 def test_gelu_epilogue_accuracy(hip_device, n, variant):
     """The GEMM's GELU alone: X = [v, 0, ...] and W[:, 0] = 1 make every pre-activation

@@ -695,38 +695,49 @@ __global__ __launch_bounds__(512) void linear_dma_kernel(LinearArgs a) {
     const __amdgpu_buffer_rsrc_t rres =
         make_rsrc(EPI == kEpiBiasResidual ? (const void*)(a.residual + m0 * N) : (const void*)a.x,
                   EPI == kEpiBiasResidual ? rows * (uint32_t)N * 4u : 0u);
+    // A row's 64 output columns of this wave are two runs of 32 (p = 0, 1), each
+    // stored by four lanes.  Plain epilogues store the two runs of a row back to
+    // back, so the halves of an output line (128 bytes at FP16) reach the memory
+    // system together (measured on a 262144 x 768 x 256 projection: 10 % faster
+    // than storing all p = 0 runs first); the residual epilogue, whose loads wait
+    // for the stores before them, keeps the p-major order (faster there).
+    h8 bhp[PN];
 #pragma unroll
     for (int p = 0; p < PN; ++p) {
       const int n = n0 + wn * 64 + 32 * p + 8 * g;
+      bhp[p] = *reinterpret_cast<const h8*>(&bias_s[n < N ? n : 0]);
+    }
+#pragma unroll
+    for (int u = 0; u < TM * PN; ++u) {
+      const int t = EPI == kEpiBiasResidual ? u % TM : u / PN;
+      const int p = EPI == kEpiBiasResidual ? u / TM : u % PN;
+      const int n = n0 + wn * 64 + 32 * p + 8 * g;
       const bool ok = n < N;
-      const h8 bh = *reinterpret_cast<const h8*>(&bias_s[ok ? n : 0]);
+      const h8 bh = bhp[p];
+      const int row = wm * 128 + 16 * t + r;
+      const uint32_t e = (uint32_t)(row * N + n);
+      float v[8];
 #pragma unroll
-      for (int t = 0; t < TM; ++t) {
-        const int row = wm * 128 + 16 * t + r;
-        const uint32_t e = (uint32_t)(row * N + n);
-        float v[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[i] = acc[p][0][t][i] + (float)bh[i];
-          v[4 + i] = acc[p][1][t][i] + (float)bh[4 + i];
-        }
-        if constexpr (EPI == kEpiBiasGelu) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] = gelu_erf(v[j]);
-        }
-        if constexpr (EPI == kEpiBiasResidual) {
-          typedef float v4 __attribute__((ext_vector_type(4)));
-          const uint32_t ro = ok ? e * 4u : 0x80000000u;
-          const v4 r0 = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(rres, ro, 0, 0));
-          const v4 r1 = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(rres, ro + 16u, 0, 0));
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            v[j] += r0[j];
-            v[4 + j] += r1[j];
-          }
-        }
-        buffer_store8(yr, ok ? e * (uint32_t)sizeof(OT) : 0x80000000u, v, Y);
+      for (int i = 0; i < 4; ++i) {
+        v[i] = acc[p][0][t][i] + (float)bh[i];
+        v[4 + i] = acc[p][1][t][i] + (float)bh[4 + i];
       }
+      if constexpr (EPI == kEpiBiasGelu) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = gelu_erf(v[j]);
+      }
+      if constexpr (EPI == kEpiBiasResidual) {
+        typedef float v4 __attribute__((ext_vector_type(4)));
+        const uint32_t ro = ok ? e * 4u : 0x80000000u;
+        const v4 r0 = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(rres, ro, 0, 0));
+        const v4 r1 = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(rres, ro + 16u, 0, 0));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] += r0[j];
+          v[4 + j] += r1[j];
+        }
+      }
+      buffer_store8(yr, ok ? e * (uint32_t)sizeof(OT) : 0x80000000u, v, Y);
     }
   };
 
