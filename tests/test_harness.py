@@ -102,8 +102,19 @@ class _Echo(torch.nn.Module):
         return x * 2
 
 
+class _EchoInto(torch.nn.Module):
+    writes_into_out = True
+
+    def forward(self, x, mask=None, *, out=None):
+        assert out is not None and out.shape == x.shape
+        out.copy_(x * 2)
+        return out
+
+
 def test_microbatch_wrappers_are_exact():
     x = torch.randn(7, 3, 2)
     full = _Echo()(x)
     assert torch.equal(harness.MicrobatchModel(_Echo(), 3)(x), full)
     assert torch.equal(harness.PreallocatedMicrobatchModel(_Echo(), 3)(x), full)
+    # a model that writes into a given tensor receives the output's slices
+    assert torch.equal(harness.PreallocatedMicrobatchModel(_EchoInto(), 3)(x), full)

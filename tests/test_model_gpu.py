@@ -177,14 +177,36 @@ def test_causality_and_batch_independence_exact(hip_device):
         assert torch.equal(part, base[10:13])
 
 
-def test_microbatched_forward_is_exact(hip_device):
-    config = TransformerConfig(24, 256, 128, 4, 128, 2, True)
+@pytest.mark.parametrize(
+    "config", [TransformerConfig(24, 256, 128, 4, 128, 2, True), TransformerConfig(20, 160, 256, 8, 512, 2, True)]
+)
+def test_microbatched_forward_is_exact(hip_device, config):
+    """Layer-tail route (d 128: microbatches copied in) and fused-FFN GEMM route (d 256: the
+    last kernel writes each microbatch's slice of the preallocated output)."""
     _, model = _build(config, hip_device)
     x, _ = harness.generate_random_case(config, hip_device, torch.float32, 8, 0.0, 1.0)
     with torch.inference_mode():
         full = model(x).clone()
         micro = harness.PreallocatedMicrobatchModel(model, 8)(x)
     assert torch.equal(full, micro)
+
+
+@pytest.mark.parametrize(
+    "config", [TransformerConfig(6, 96, 128, 4, 128, 2, True), TransformerConfig(6, 80, 256, 8, 512, 2, True)]
+)
+@pytest.mark.parametrize("padding", [0.0, 0.25])
+def test_forward_into_out_is_exact(hip_device, config, padding):
+    print(f"\n[out=] {config} padding={padding}", flush=True)
+    _, model = _build(config, hip_device)
+    x, mask = harness.generate_random_case(config, hip_device, torch.float32, 3, padding, 1.0)
+    with torch.inference_mode():
+        ref = model(x, mask).clone()
+        buf = torch.full_like(x, float("nan"))
+        got = model(x, mask, out=buf)
+        assert got.data_ptr() == buf.data_ptr()
+        assert torch.equal(got, ref)
+        with pytest.raises(ValueError):
+            model(x, mask, out=torch.empty_like(x, dtype=torch.float16))
 
 
 def test_hip_graph_replays_match_eager(hip_device):

@@ -244,6 +244,36 @@ def _(x, w_in, b_in, w_out, b_out, residual, gamma, beta, eps, out_dtype, varian
     return torch.empty_like(residual), residual.new_empty(residual.shape, dtype=_dtype(out_dtype))
 
 
+@torch.library.custom_op("mpk::ffn_residual_layer_norm_into", mutates_args=("normalized",))
+def ffn_residual_layer_norm_into(
+    x: torch.Tensor, w_in: torch.Tensor, b_in: torch.Tensor, w_out: torch.Tensor, b_out: torch.Tensor,
+    residual: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float, variant: int,
+    normalized: torch.Tensor,
+) -> torch.Tensor:
+    """``ffn_residual_layer_norm`` with the normalized output written into ``normalized``
+    (contiguous, residual's shape, FP32 or FP16: a caller's preallocated output slice, so
+    no copy follows); returns the residual output."""
+    f, d = w_in.shape
+    residual_out = torch.empty_like(residual)
+    _require_aligned("unsupported fused FFN inputs", x, w_in, b_in, w_out, b_out, residual, gamma, beta, residual_out,
+                     normalized)
+    _lib.check(
+        _lib.load().mpk_ffn_residual_layernorm(
+            x.data_ptr(), _lib.dtype_code(x.dtype), w_in.data_ptr(), b_in.data_ptr(), w_out.data_ptr(),
+            b_out.data_ptr(), residual.data_ptr(), gamma.data_ptr(), beta.data_ptr(), residual_out.data_ptr(),
+            normalized.data_ptr(), _lib.dtype_code(normalized.dtype), _rows(x, d), d, f, float(eps), int(variant),
+            _lib.stream_handle(x.device),
+        ),
+        "mpk_ffn_residual_layernorm",
+    )
+    return residual_out
+
+
+@ffn_residual_layer_norm_into.register_fake
+def _(x, w_in, b_in, w_out, b_out, residual, gamma, beta, eps, variant, normalized):
+    return torch.empty_like(residual)
+
+
 # --------------------------------------------------------------------------- attention
 
 

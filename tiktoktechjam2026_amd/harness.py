@@ -469,10 +469,16 @@ class PreallocatedMicrobatchModel(nn.Module):
         if out is None or out.shape != x.shape or out.device != x.device:
             out = torch.empty_like(x, dtype=torch.float32)
             self._output = out
+        # a model that can write its result into a given tensor fills the slice directly
+        # (same values, no copy); others are copied in as the reference does
+        direct = getattr(self.model, "writes_into_out", False)
         for start in range(0, x.shape[0], self.microbatch_size):
             end = min(start + self.microbatch_size, x.shape[0])
             mask = None if valid_token_mask is None else valid_token_mask[start:end]
-            out[start:end].copy_(self.model(x[start:end], mask))
+            if direct:
+                self.model(x[start:end], mask, out=out[start:end])
+            else:
+                out[start:end].copy_(self.model(x[start:end], mask))
         return out
 
 

@@ -212,8 +212,11 @@ def mixed_ffn_add_layer_norm(
     num_stages: int = 2,
     normalized_dtype: torch.dtype = torch.float32,
     variant: int = 0,
+    out: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Whole FFN (exact GELU on the FP32 accumulator) + residual + LayerNorm; returns ``(R', N')``."""
+    """Whole FFN (exact GELU on the FP32 accumulator) + residual + LayerNorm; returns ``(R', N')``.
+    ``out``: optional contiguous tensor of ``residual``'s shape and ``normalized_dtype`` that
+    receives N' (then returned as N')."""
     d = x.shape[-1] if x.dim() > 0 else 0
     if not (
         _gpu(x)
@@ -230,8 +233,18 @@ def mixed_ffn_add_layer_norm(
         and _fp16_linear_ok(linear_out)
         and _norm_ok(norm, d)
         and normalized_dtype in (torch.float16, torch.float32)
+        and (
+            out is None
+            or (_gpu(out) and out.dtype == normalized_dtype and out.shape == residual.shape and out.is_contiguous())
+        )
     ):
         raise ValueError("unsupported fused FFN inputs")
+    if out is not None:
+        residual_out = _ops.ffn_residual_layer_norm_into(
+            x, linear_in.weight, linear_in.bias, linear_out.weight, linear_out.bias, residual, norm.weight,
+            norm.bias, float(norm.eps), int(variant), out,
+        )
+        return residual_out, out
     return _ops.ffn_residual_layer_norm(
         x, linear_in.weight, linear_in.bias, linear_out.weight, linear_out.bias, residual, norm.weight, norm.bias,
         float(norm.eps), _code(normalized_dtype), int(variant),

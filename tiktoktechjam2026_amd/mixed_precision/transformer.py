@@ -135,14 +135,16 @@ class MixedPrecisionTransformerBlock(nn.Module):
         self.ffn_out.half()
 
     def ffn(
-        self, normalized_ffn: torch.Tensor, residual: torch.Tensor, next_norm: nn.LayerNorm, out_dtype: torch.dtype
+        self, normalized_ffn: torch.Tensor, residual: torch.Tensor, next_norm: nn.LayerNorm, out_dtype: torch.dtype,
+        out: Optional[torch.Tensor] = None,
     ):
-        """FFN + residual + next LayerNorm -> ``(x', next_norm(x'))``."""
+        """FFN + residual + next LayerNorm -> ``(x', next_norm(x'))``; the fused route writes
+        next_norm(x') into ``out`` when one is given (other routes leave ``out`` to the caller)."""
         route = self.route
         if route.fuse_full_ffn:
             return mixed_ffn_add_layer_norm(
                 normalized_ffn, self.ffn_in, self.ffn_out, residual, next_norm,
-                normalized_dtype=out_dtype, variant=route.ffn_variant,
+                normalized_dtype=out_dtype, variant=route.ffn_variant, out=out,
             )
         activated = mixed_linear(
             normalized_ffn, self.ffn_in, output_dtype=torch.float16, fuse_gelu=True, variant=route.ffn_in_variant
@@ -216,7 +218,29 @@ class MixedPrecisionTransformer(nn.Module):
         """1 + 2L launches: LayerNorm+QKV, then per layer attention and the fused layer tail."""
         return _forward_layer_tail_impl(self, x, key_valid, causal)
 
-    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    # forward(..., out=t) writes the result into t (see forward); the microbatching harness
+    # uses it to fill its preallocated output without a copy
+    writes_into_out = True
+
+    def forward(
+        self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None, *, out: Optional[torch.Tensor] = None
+    ) -> torch.Tensor:
+        """The reference's forward; with ``out`` (contiguous FP32, x's shape) the result is
+        written there and ``out`` is returned - on the GEMM route with the fused FFN the last
+        layer's kernel stores it directly, elsewhere it is copied in."""
+        if out is not None and not (
+            out.dtype == torch.float32 and out.shape == x.shape and out.is_contiguous() and out.device == x.device
+        ):
+            raise ValueError("out must be a contiguous FP32 tensor of the input's shape on its device")
+        result = self._forward(x, valid_token_mask, out)
+        if out is not None and result.data_ptr() != out.data_ptr():
+            out.copy_(result)
+            return out
+        return result
+
+    def _forward(
+        self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor], out: Optional[torch.Tensor]
+    ) -> torch.Tensor:
         if x.dtype != torch.float32:
             raise ValueError("mixed candidate requires an FP32 input/residual stream")
         if not x.is_cuda:
@@ -243,9 +267,13 @@ class MixedPrecisionTransformer(nn.Module):
             )
             last = index + 1 == n_layers
             next_norm = self.final_norm if last else self.layers[index + 1].norm1
-            x, normalized = layer.ffn(normalized_ffn, x, next_norm, torch.float32 if last else stream_dtype)
+            x, normalized = layer.ffn(
+                normalized_ffn, x, next_norm, torch.float32 if last else stream_dtype, out=out if last else None
+            )
 
         if effective_mask is not None:
+            if normalized.data_ptr() == (out.data_ptr() if out is not None else -1):
+                return normalized.masked_fill_(~effective_mask[..., None], 0)
             return normalized.masked_fill(~effective_mask[..., None], 0)
         return normalized
 
