@@ -111,6 +111,8 @@ int mpk_linear_add_layernorm(const void* x, int x_dtype, const void* w, const vo
  *   normalized_out = LayerNorm(residual_out) * gamma + beta
  * x: [m, d]; w_in: [f, d] FP16; b_in: [f] FP16; w_out: [d, f] FP16;
  * b_out: [d] FP16.  d in {32, 64, 128, 256, 512}; f % 32 == 0.
+ * residual_out may be NULL: then only normalized_out is stored (a last layer,
+ * whose residual stream nothing reads).
  * variant: 0 = built-in choice (mpk_ffn_residual_layernorm_auto_variant),
  * 1 / 2 = one / two 16-token tiles per wave, 3 = the wide kernel (d 256,
  * f <= 8192, one wave per SIMD), 4 = the role-split wide kernel (same shapes;

@@ -348,6 +348,19 @@ def _check_ffn(hip_device, d, f, m, variant, x_dtype):
         _close(r_out, r64, atol, 1e-5, "ffn residual_out")
         tol = max(atol * 10, 1e-4) if out_dtype == torch.float32 else 2 ** -9
         _close(n_out, _ln64(r64, norm), tol, tol, "ffn normalized_out")
+        # a last layer: N' written into a given tensor, or returned alone, with R' not stored
+        # (residual_out NULL at the C ABI) - the same N' bit for bit
+        buf = torch.full_like(n_out, float("nan"))
+        r_none, n_into = mixed_ffn_add_layer_norm(
+            x.to(hip_device, x_dtype), lin_in, lin_out, resid.to(hip_device), norm,
+            normalized_dtype=out_dtype, variant=variant, out=buf, store_residual=False,
+        )
+        assert r_none is None and n_into.data_ptr() == buf.data_ptr() and torch.equal(buf, n_out)
+        r_none, n_final = mixed_ffn_add_layer_norm(
+            x.to(hip_device, x_dtype), lin_in, lin_out, resid.to(hip_device), norm,
+            normalized_dtype=out_dtype, variant=variant, store_residual=False,
+        )
+        assert r_none is None and torch.equal(n_final, n_out)
 
 
 def test_fused_ops_reject_unsupported(hip_device):

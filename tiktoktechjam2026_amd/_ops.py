@@ -248,19 +248,21 @@ def _(x, w_in, b_in, w_out, b_out, residual, gamma, beta, eps, out_dtype, varian
 def ffn_residual_layer_norm_into(
     x: torch.Tensor, w_in: torch.Tensor, b_in: torch.Tensor, w_out: torch.Tensor, b_out: torch.Tensor,
     residual: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float, variant: int,
-    normalized: torch.Tensor,
+    normalized: torch.Tensor, store_residual: bool,
 ) -> torch.Tensor:
     """``ffn_residual_layer_norm`` with the normalized output written into ``normalized``
     (contiguous, residual's shape, FP32 or FP16: a caller's preallocated output slice, so
-    no copy follows); returns the residual output."""
+    no copy follows); returns the residual output, or an empty tensor when
+    ``store_residual`` is false (the kernel then stores only the normalized output)."""
     f, d = w_in.shape
-    residual_out = torch.empty_like(residual)
+    residual_out = torch.empty_like(residual) if store_residual else residual.new_empty(0)
     _require_aligned("unsupported fused FFN inputs", x, w_in, b_in, w_out, b_out, residual, gamma, beta, residual_out,
                      normalized)
     _lib.check(
         _lib.load().mpk_ffn_residual_layernorm(
             x.data_ptr(), _lib.dtype_code(x.dtype), w_in.data_ptr(), b_in.data_ptr(), w_out.data_ptr(),
-            b_out.data_ptr(), residual.data_ptr(), gamma.data_ptr(), beta.data_ptr(), residual_out.data_ptr(),
+            b_out.data_ptr(), residual.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
+            residual_out.data_ptr() if store_residual else None,
             normalized.data_ptr(), _lib.dtype_code(normalized.dtype), _rows(x, d), d, f, float(eps), int(variant),
             _lib.stream_handle(x.device),
         ),
@@ -270,8 +272,25 @@ def ffn_residual_layer_norm_into(
 
 
 @ffn_residual_layer_norm_into.register_fake
-def _(x, w_in, b_in, w_out, b_out, residual, gamma, beta, eps, variant, normalized):
-    return torch.empty_like(residual)
+def _(x, w_in, b_in, w_out, b_out, residual, gamma, beta, eps, variant, normalized, store_residual):
+    return torch.empty_like(residual) if store_residual else residual.new_empty(0)
+
+
+@torch.library.custom_op("mpk::ffn_residual_layer_norm_final", mutates_args=())
+def ffn_residual_layer_norm_final(
+    x: torch.Tensor, w_in: torch.Tensor, b_in: torch.Tensor, w_out: torch.Tensor, b_out: torch.Tensor,
+    residual: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float, out_dtype: int, variant: int,
+) -> torch.Tensor:
+    """``ffn_residual_layer_norm`` for a last layer: only the normalized output is stored and
+    returned (the residual stream after it is not read)."""
+    normalized = torch.empty(residual.shape, device=x.device, dtype=_dtype(out_dtype))
+    ffn_residual_layer_norm_into(x, w_in, b_in, w_out, b_out, residual, gamma, beta, eps, variant, normalized, False)
+    return normalized
+
+
+@ffn_residual_layer_norm_final.register_fake
+def _(x, w_in, b_in, w_out, b_out, residual, gamma, beta, eps, out_dtype, variant):
+    return residual.new_empty(residual.shape, dtype=_dtype(out_dtype))
 
 
 # --------------------------------------------------------------------------- attention

@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kBlock) void ffn_ln_kernel(FfnArgs a) {
             v[i] = yacc[p][0][t][i];
             v[4 + i] = yacc[p][1][t][i];
           }
-          store8(a.residual_out + m * D + n, v);
+          if (a.residual_out) store8(a.residual_out + m * D + n, v);
           load8_f32(a.gamma + n, gm);
           load8_f32(a.beta + n, bt);
 #pragma unroll
@@ -256,7 +256,7 @@ extern "C" int mpk_ffn_residual_layernorm(const void* x, int x_dtype, const void
                                           const float* gamma, const float* beta, float* residual_out,
                                           void* normalized_out, int normalized_dtype, int64_t m, int32_t d,
                                           int32_t f, float eps, int variant, void* stream) {
-  if (!x || !w_in || !b_in || !w_out || !b_out || !residual || !gamma || !beta || !residual_out ||
+  if (!x || !w_in || !b_in || !w_out || !b_out || !residual || !gamma || !beta ||
       !normalized_out || m < 0 || d <= 0 || f <= 0)
     return MPK_EINVAL;
   if ((x_dtype != kF32 && x_dtype != kF16) || (normalized_dtype != kF32 && normalized_dtype != kF16))
@@ -264,7 +264,7 @@ extern "C" int mpk_ffn_residual_layernorm(const void* x, int x_dtype, const void
   if (d != 32 && d != 64 && d != 128 && d != 256 && d != 512) return MPK_EUNSUPPORTED;
   if (f % 32 != 0) return MPK_EUNSUPPORTED;
   if (!aligned16(x) || !aligned16(w_in) || !aligned16(b_in) || !aligned16(w_out) || !aligned16(b_out) ||
-      !aligned16(residual) || !aligned16(gamma) || !aligned16(beta) || !aligned16(residual_out) ||
+      !aligned16(residual) || !aligned16(gamma) || !aligned16(beta) || (residual_out && !aligned16(residual_out)) ||
       !aligned16(normalized_out))
     return MPK_EALIGN;
   if (m == 0) return MPK_OK;

@@ -346,7 +346,10 @@ __global__ __launch_bounds__(kNT, 1) void ffn_wide_kernel(FfnArgs a) {
     const int64_t row0 = tile * kTok + 32 * wave;
     const uint32_t rows = (uint32_t)max<int64_t>(0, min<int64_t>(32, M - row0));
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.residual + row0 * D, rows * (uint32_t)(D * 4));
-    const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.residual_out + row0 * D, rows * (uint32_t)(D * 4));
+    // residual_out NULL: a zero-size resource drops the stores, which still issue (the
+    // copy waits count them)
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.residual_out ? a.residual_out + row0 * D : nullptr,
+                                                a.residual_out ? rows * (uint32_t)(D * 4) : 0u);
     const __amdgpu_buffer_rsrc_t no =
         make_rsrc(static_cast<OT*>(a.normalized_out) + row0 * D, rows * (uint32_t)(D * sizeof(OT)));
     const float* bo = prm;
@@ -694,7 +697,10 @@ __global__ __launch_bounds__(kRT) void ffn_roles_kernel(FfnArgs a) {
     const int64_t row0 = t * kTok + 32 * sl;
     const uint32_t rows = (uint32_t)max<int64_t>(0, min<int64_t>(32, M - row0));
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.residual + row0 * D, rows * (uint32_t)(D * 4));
-    const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.residual_out + row0 * D, rows * (uint32_t)(D * 4));
+    // residual_out NULL: a zero-size resource drops the stores, which still issue (the
+    // copy waits count them)
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.residual_out ? a.residual_out + row0 * D : nullptr,
+                                                a.residual_out ? rows * (uint32_t)(D * 4) : 0u);
     const __amdgpu_buffer_rsrc_t no =
         make_rsrc(static_cast<OT*>(a.normalized_out) + row0 * D, rows * (uint32_t)(D * sizeof(OT)));
     const float* bo = prm;

@@ -213,10 +213,11 @@ def mixed_ffn_add_layer_norm(
     normalized_dtype: torch.dtype = torch.float32,
     variant: int = 0,
     out: Optional[torch.Tensor] = None,
-) -> Tuple[torch.Tensor, torch.Tensor]:
+    store_residual: bool = True,
+) -> Tuple[Optional[torch.Tensor], torch.Tensor]:
     """Whole FFN (exact GELU on the FP32 accumulator) + residual + LayerNorm; returns ``(R', N')``.
     ``out``: optional contiguous tensor of ``residual``'s shape and ``normalized_dtype`` that
-    receives N' (then returned as N')."""
+    receives N' (then returned as N'); ``store_residual=False`` skips R' (returned as None)."""
     d = x.shape[-1] if x.dim() > 0 else 0
     if not (
         _gpu(x)
@@ -237,14 +238,20 @@ def mixed_ffn_add_layer_norm(
             out is None
             or (_gpu(out) and out.dtype == normalized_dtype and out.shape == residual.shape and out.is_contiguous())
         )
+
     ):
         raise ValueError("unsupported fused FFN inputs")
     if out is not None:
         residual_out = _ops.ffn_residual_layer_norm_into(
             x, linear_in.weight, linear_in.bias, linear_out.weight, linear_out.bias, residual, norm.weight,
-            norm.bias, float(norm.eps), int(variant), out,
+            norm.bias, float(norm.eps), int(variant), out, bool(store_residual),
         )
-        return residual_out, out
+        return (residual_out if store_residual else None), out
+    if not store_residual:
+        return None, _ops.ffn_residual_layer_norm_final(
+            x, linear_in.weight, linear_in.bias, linear_out.weight, linear_out.bias, residual, norm.weight,
+            norm.bias, float(norm.eps), _code(normalized_dtype), int(variant),
+        )
     return _ops.ffn_residual_layer_norm(
         x, linear_in.weight, linear_in.bias, linear_out.weight, linear_out.bias, residual, norm.weight, norm.bias,
         float(norm.eps), _code(normalized_dtype), int(variant),

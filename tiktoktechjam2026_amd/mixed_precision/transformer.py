@@ -136,15 +136,16 @@ class MixedPrecisionTransformerBlock(nn.Module):
 
     def ffn(
         self, normalized_ffn: torch.Tensor, residual: torch.Tensor, next_norm: nn.LayerNorm, out_dtype: torch.dtype,
-        out: Optional[torch.Tensor] = None,
+        out: Optional[torch.Tensor] = None, last: bool = False,
     ):
-        """FFN + residual + next LayerNorm -> ``(x', next_norm(x'))``; the fused route writes
-        next_norm(x') into ``out`` when one is given (other routes leave ``out`` to the caller)."""
+        """FFN + residual + next LayerNorm -> ``(x', next_norm(x'))``.  On the fused route the
+        last layer skips x', which nothing reads (returned as None), and writes
+        next_norm(x') into ``out`` when one is given; other routes ignore both."""
         route = self.route
         if route.fuse_full_ffn:
             return mixed_ffn_add_layer_norm(
                 normalized_ffn, self.ffn_in, self.ffn_out, residual, next_norm,
-                normalized_dtype=out_dtype, variant=route.ffn_variant, out=out,
+                normalized_dtype=out_dtype, variant=route.ffn_variant, out=out, store_residual=not last,
             )
         activated = mixed_linear(
             normalized_ffn, self.ffn_in, output_dtype=torch.float16, fuse_gelu=True, variant=route.ffn_in_variant
@@ -268,7 +269,8 @@ class MixedPrecisionTransformer(nn.Module):
             last = index + 1 == n_layers
             next_norm = self.final_norm if last else self.layers[index + 1].norm1
             x, normalized = layer.ffn(
-                normalized_ffn, x, next_norm, torch.float32 if last else stream_dtype, out=out if last else None
+                normalized_ffn, x, next_norm, torch.float32 if last else stream_dtype, out=out if last else None,
+                last=last,
             )
 
         if effective_mask is not None:
