@@ -115,9 +115,9 @@ int mpk_linear_add_layernorm(const void* x, int x_dtype, const void* w, const vo
  * whose residual stream nothing reads).
  * variant: 0 = built-in choice (mpk_ffn_residual_layernorm_auto_variant),
  * 1 / 2 = one / two 16-token tiles per wave, 3 = the wide kernel (d 256,
- * f <= 8192, one wave per SIMD), 4 = the role-split wide kernel (same shapes;
- * a vector wave and a matrix wave per SIMD).  Variants 3 and 4 give identical
- * results.
+ * f <= 8192, one wave per SIMD, FP16 x only: MPK_EUNSUPPORTED for FP32 x),
+ * 4 = the role-split wide kernel (same shapes, FP16 or FP32 x; a vector wave
+ * and a matrix wave per SIMD).  Variants 3 and 4 give identical results.
  * Replaces: mixed_ffn_add_layer_norm (mixed_precision/triton_linear.py:327-378).
  */
 int mpk_ffn_residual_layernorm(const void* x, int x_dtype, const void* w_in, const void* b_in,

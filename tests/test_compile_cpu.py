@@ -28,7 +28,7 @@ ALLOWED = ("mpk.", "aten.sym_size", "<built-in function getitem>")
 VIEWS = {"view", "permute", "unbind", "contiguous"}
 
 
-def _export(config, masked: bool):
+def _export(config, masked: bool, with_out: bool = False):
     model = MixedPrecisionTransformer(config).eval()
     model.convert_projections_to_fp16()
     model.assume_all_tokens_valid = not masked
@@ -38,7 +38,10 @@ def _export(config, masked: bool):
         args = (x,)
         if masked:
             args = (x, torch.ones(config.batch_size, config.seq_len, dtype=torch.bool, device="cuda"))
-        graph_module, _ = torch._dynamo.export(model)(*args)
+        kwargs = {}
+        if with_out:
+            kwargs["out"] = torch.empty(config.batch_size, config.seq_len, config.d_model, device="cuda")
+        graph_module, _ = torch._dynamo.export(model)(*args, **kwargs)
     return [str(n.target) for n in graph_module.graph.nodes if n.op in ("call_function", "call_method")]
 
 
@@ -58,3 +61,14 @@ def test_masked_forward_exports_too():
     targets = _export(config, masked=True)
     assert targets.count("mpk.attention.default") == 2
     assert any("masked_fill" in t for t in targets)
+
+
+@pytest.mark.parametrize("name", ["gemm_ln_epilogue_d256", "layer_tail_d128"])
+def test_forward_with_out_exports_as_one_graph(name):
+    """``forward(x, None, out=t)`` (the microbatch harness's direct-write call) traces too."""
+    config, expected = ROUTES[name]
+    targets = _export(config, masked=False, with_out=True)
+    strays = [t for t in targets if not t.startswith(ALLOWED) and t not in VIEWS and "copy_" not in t]
+    assert not strays, f"non-library computation in the traced forward: {strays}"
+    for op, count in expected.items():
+        assert targets.count(op) == count, (op, targets)

@@ -118,3 +118,48 @@ def test_microbatch_wrappers_are_exact():
     assert torch.equal(harness.PreallocatedMicrobatchModel(_Echo(), 3)(x), full)
     # a model that writes into a given tensor receives the output's slices
     assert torch.equal(harness.PreallocatedMicrobatchModel(_EchoInto(), 3)(x), full)
+
+
+def test_preallocated_microbatch_returns_a_fresh_output_per_call():
+    """``mixed_precision_benchmark.py:26`` allocates the output inside forward: a caller that
+    keeps two results must see both unchanged."""
+    for model in (_Echo(), _EchoInto()):
+        runner = harness.PreallocatedMicrobatchModel(model, 3)
+        x1, x2 = torch.randn(7, 3, 2), torch.randn(7, 3, 2)
+        first = runner(x1)
+        second = runner(x2)
+        assert first.data_ptr() != second.data_ptr()
+        assert torch.equal(first, x1 * 2) and torch.equal(second, x2 * 2)
+
+
+class _Wrapper(torch.nn.Module):
+    """Stands in for torch.compile's wrapper, which forwards instance attribute reads."""
+
+    def __init__(self, inner):
+        super().__init__()
+        self.inner = inner
+
+    def __getattr__(self, name):
+        if name == "writes_into_out":
+            return getattr(self.inner, name)
+        return super().__getattr__(name)
+
+    def forward(self, x, mask=None):
+        return self.inner(x, mask)
+
+
+def test_preallocated_microbatch_copies_through_wrappers():
+    """A wrapped module (a compiled graph) is called without ``out=``, as in the reference."""
+    x = torch.randn(7, 3, 2)
+    wrapped = _Wrapper(_EchoInto())
+    assert wrapped.writes_into_out
+    calls = []
+    inner = wrapped.inner
+
+    def forward(x, mask=None, *, out=None):
+        calls.append(out is None)
+        return x * 2
+
+    inner.forward = forward
+    assert torch.equal(harness.PreallocatedMicrobatchModel(wrapped, 3)(x), x * 2)
+    assert calls and all(calls)

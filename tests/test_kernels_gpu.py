@@ -319,9 +319,21 @@ def test_ffn_wide_residual_layernorm(hip_device, f, m, variant):
     _check_ffn(hip_device, 256, f, m, variant, torch.float16)
 
 
-@pytest.mark.parametrize("variant", [3, 4])
-def test_ffn_wide_fp32_input(hip_device, variant):
-    _check_ffn(hip_device, 256, 1024, 777, variant, torch.float32)
+def test_ffn_wide_fp32_input(hip_device):
+    _check_ffn(hip_device, 256, 1024, 777, 4, torch.float32)
+
+
+def test_ffn_wide_one_wave_rejects_fp32_input(hip_device):
+    """Variant 3 (one wave per SIMD) would spill with FP32 X: the library returns
+    MPK_EUNSUPPORTED for it before any launch."""
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_ffn_add_layer_norm
+
+    x = torch.zeros(64, 256, device=hip_device)
+    with pytest.raises(RuntimeError, match="1002"):
+        mixed_ffn_add_layer_norm(
+            x, _linear(256, 1024, hip_device, 31), _linear(1024, 256, hip_device, 32), torch.zeros_like(x),
+            _norm(256, hip_device, 33), normalized_dtype=torch.float16, variant=3,
+        )
 
 
 def _check_ffn(hip_device, d, f, m, variant, x_dtype):

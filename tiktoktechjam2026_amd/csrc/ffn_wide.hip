@@ -839,11 +839,11 @@ hipError_t launch_ffn_roles(const FfnArgs& a, int d, int w_dtype, int x_dtype, i
   return of ? launch_roles<256, _Float16, float>(a, s) : launch_roles<256, _Float16, _Float16>(a, s);
 }
 
+// The one-wave kernel takes FP16 X only: with FP32 X its tile loads need more registers than
+// the 32 x D accumulators leave, and it would spill.  FP32 X runs on variant 4.
 hipError_t launch_ffn_wide(const FfnArgs& a, int d, int w_dtype, int x_dtype, int out_dtype, hipStream_t s) {
-  if (w_dtype != kF16 || !ffn_wide_supported(d, a.f)) return (hipError_t)MPK_EUNSUPPORTED;
-  const bool xf = x_dtype == kF32, of = out_dtype == kF32;
-  if (xf) return of ? launch_wide<256, float, float>(a, s) : launch_wide<256, float, _Float16>(a, s);
-  return of ? launch_wide<256, _Float16, float>(a, s) : launch_wide<256, _Float16, _Float16>(a, s);
+  if (w_dtype != kF16 || x_dtype != kF16 || !ffn_wide_supported(d, a.f)) return (hipError_t)MPK_EUNSUPPORTED;
+  return out_dtype == kF32 ? launch_wide<256, _Float16, float>(a, s) : launch_wide<256, _Float16, _Float16>(a, s);
 }
 
 }  // namespace mpk

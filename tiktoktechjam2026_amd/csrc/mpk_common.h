@@ -250,9 +250,11 @@ typedef __attribute__((address_space(3))) void lds_void;
 // (lds_base wave-uniform, in M0).  Issued as inline assembly: the compiler does
 // not track it, so it neither counts it in its own vmcnt waits nor drains every
 // LDS read behind it (it cannot tell the copy's target buffer from the ones being
-// read).  Its completion is awaited explicitly with wait_copies.
+// read).  Its completion is awaited explicitly with wait_copies.  M0 is declared
+// clobbered, so the compiler keeps no value of its own there across a copy.
 __device__ __forceinline__ void dma16(uint32_t voff, const void* base, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "s"(lds_base));
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "s"(lds_base)
+               : "m0");
 }
 
 // Wait until at most N of this wave's vector-memory operations are outstanding

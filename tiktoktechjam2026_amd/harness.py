@@ -454,24 +454,25 @@ class MicrobatchModel(nn.Module):
 
 
 class PreallocatedMicrobatchModel(nn.Module):
-    """Microbatched forward into one preallocated FP32 output (``mixed_precision_benchmark.py:13-33``)."""
+    """Microbatched forward into one FP32 output allocated per call (``mixed_precision_benchmark.py:13-33``).
+
+    As in the reference, every call returns a tensor of its own (``torch.empty_like``, served
+    by the caching allocator), so results kept from earlier calls are never overwritten."""
 
     def __init__(self, model: nn.Module, microbatch_size: int) -> None:
         super().__init__()
         self.model = model
         self.microbatch_size = microbatch_size
-        self._output: Optional[torch.Tensor] = None
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         if x.shape[0] <= self.microbatch_size:
             return self.model(x, valid_token_mask)
-        out = self._output
-        if out is None or out.shape != x.shape or out.device != x.device:
-            out = torch.empty_like(x, dtype=torch.float32)
-            self._output = out
-        # a model that can write its result into a given tensor fills the slice directly
-        # (same values, no copy); others are copied in as the reference does
-        direct = getattr(self.model, "writes_into_out", False)
+        out = torch.empty_like(x, dtype=torch.float32)
+        # A module that can write its result into a given tensor fills each slice directly (same
+        # values, no copy); any other model, including a ``torch.compile`` wrapper around such a
+        # module (the class attribute is looked up on the wrapper's own type, so a compiled graph
+        # is never handed an output to mutate), is copied in as the reference does.
+        direct = bool(getattr(type(self.model), "writes_into_out", False))
         for start in range(0, x.shape[0], self.microbatch_size):
             end = min(start + self.microbatch_size, x.shape[0])
             mask = None if valid_token_mask is None else valid_token_mask[start:end]

@@ -234,7 +234,8 @@ class MixedPrecisionTransformer(nn.Module):
         ):
             raise ValueError("out must be a contiguous FP32 tensor of the input's shape on its device")
         result = self._forward(x, valid_token_mask, out)
-        if out is not None and result.data_ptr() != out.data_ptr():
+        # identity, not data_ptr(): Dynamo traces an ``is`` test, but not a pointer comparison
+        if out is not None and result is not out:
             out.copy_(result)
             return out
         return result
@@ -274,7 +275,7 @@ class MixedPrecisionTransformer(nn.Module):
             )
 
         if effective_mask is not None:
-            if normalized.data_ptr() == (out.data_ptr() if out is not None else -1):
+            if out is not None and normalized is out:
                 return normalized.masked_fill_(~effective_mask[..., None], 0)
             return normalized.masked_fill(~effective_mask[..., None], 0)
         return normalized
