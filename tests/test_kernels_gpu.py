@@ -495,6 +495,32 @@ def test_attention_rising_scores(hip_device, variant, pattern):
         _close(out, _ref_attention(q, k, v, scale, True), 3e-3, 3e-3, f"rising scores ({pattern})")
 
 
+@pytest.mark.parametrize("variant", [6, 7])
+def test_attention_32x32_grouped_schedule(hip_device, variant):
+    """A launch with at least 1024 workgroups per XCD walks its (batch, head) rows in groups
+    of 8 (B 64 x H 8 = 512 rows; S 2048 gives 16 query blocks of 128 for variant 6, S 4096
+    16 blocks of 256 for variant 7).  Batch rows are independent and a block's arithmetic
+    does not depend on when it runs, so the grouped launch must equal, bit for bit, eight
+    launches of 8 sequences each (64 rows: too few workgroups for grouping); two rows are
+    also checked against float64."""
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention
+
+    b, h, hd = 64, 8, 32
+    s = 2048 if variant == 6 else 4096
+    print(f"\n[attention grouped] b={b} h={h} s={s} variant={variant}", flush=True)
+    torch.manual_seed(5)
+    qkv = (torch.randn(b, s, 3, h, hd) * 1.5).to(hip_device, torch.float16)
+    q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+    grouped = attention(q, k, v, hd ** -0.5, causal=True, variant=variant)
+    for b0 in range(0, b, 8):
+        part = attention(q[b0:b0 + 8], k[b0:b0 + 8], v[b0:b0 + 8], hd ** -0.5, causal=True, variant=variant)
+        assert torch.equal(grouped[b0:b0 + 8], part), f"sequences {b0}..{b0 + 7} differ"
+    for row in (9, 500):
+        bi, hi = divmod(row, h)
+        ref = _ref_attention(q[bi:bi + 1, hi:hi + 1], k[bi:bi + 1, hi:hi + 1], v[bi:bi + 1, hi:hi + 1], hd ** -0.5, True)
+        _close(grouped[bi:bi + 1, :, hi:hi + 1], ref, 3e-3, 3e-3, f"grouped attention row {row}")
+
+
 def test_attention_32x32_rejects_other_head_dims(hip_device):
     from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention
 
