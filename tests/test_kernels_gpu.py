@@ -546,6 +546,42 @@ def test_attention_noncausal_fp32io_and_keymask(hip_device, b, h, s, hd):
     _close(out_m, ref_m, 3e-3, 3e-3, "causal + key mask")
 
 
+@pytest.mark.parametrize(
+    "hd,variant", [(32, 1), (32, 6), (32, 7), (64, 6), (64, 2), (16, 1), (8, 1), (128, 1), (256, 1)]
+)
+@pytest.mark.parametrize("mags", [(1e5, 1e-5, 1e5), (1e-6, 1e6, 1e-6), (1e5, 1e-5, 1e-6)])
+def test_attention_fp32io_exponent_range(hip_device, hd, variant, mags):
+    """FP32 inputs far outside FP16's normal range (about 6e-5 .. 65504), as the reference's
+    TF32 kernel accepts them: |q| up to ~5e5 with |k| ~ 1e-5 (scores stay O(1), so the
+    softmax is not degenerate), the mirror image, and v below FP16's normal range.  The
+    kernels scale q, k and v by powers of two before rounding them to FP16, so nothing
+    overflows or loses precision to subnormals; compared with float64 on the unrounded
+    FP32 values, relative to the size of v."""
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention
+
+    b, h, s = 2, 2, 300
+    sq, sk, sv = mags
+    print(f"\n[attention fp32 range] hd={hd} variant={variant} q~{sq:g} k~{sk:g} v~{sv:g}", flush=True)
+    g = torch.Generator().manual_seed(61)
+    qkv = torch.randn(b, s, 3, h, hd, generator=g)
+    qkv[:, :, 0] *= sq
+    qkv[:, :, 1] *= sk
+    qkv[:, :, 2] *= sv
+    qkv = qkv.to(hip_device)
+    q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+    scale = hd ** -0.5
+    for causal in (True, False):
+        out = attention(q, k, v, scale, causal=causal, variant=variant)
+        assert out.dtype == torch.float32 and torch.isfinite(out).all()
+        q64, k64, v64 = (t.detach().cpu().double() for t in (q, k, v))
+        sc = (q64 @ k64.transpose(-1, -2)) * scale
+        if causal:
+            sc = sc.masked_fill(torch.ones(s, s, dtype=torch.bool).triu(1), float("-inf"))
+        ref = (torch.softmax(sc, dim=-1) @ v64).permute(0, 2, 1, 3)
+        err = (out.cpu().double() - ref).abs().max().item()
+        assert err <= 3e-3 * sv, f"max error {err:g} against |v| ~ {sv:g} (causal={causal})"
+
+
 def test_attention_causality_exact(hip_device):
     """Output row t is bit-identical when keys/values after t change."""
     from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention

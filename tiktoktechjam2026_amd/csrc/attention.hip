@@ -12,8 +12,9 @@
 // l sums the same FP16-rounded probabilities that weight V (the reference sums the
 // unrounded FP32 p_j); the two sums differ by at most 2^-12 relative (half an FP16
 // ulp of o), and this way the weights applied to V sum to exactly one.
-// For FP32 inputs (the reference's TF32 kernel) q, k, v are rounded to FP16 on
-// load, which keeps the same 10-bit operand mantissa as TF32.
+// For FP32 inputs (the reference's TF32 kernel) q, k and v are scaled by powers of
+// two into FP16's range and then rounded to FP16, which keeps TF32's 10-bit operand
+// mantissa and, through the scales, FP32's exponent range (see f32_scale_exp).
 //
 // Structure.  A workgroup of NW waves owns QB = 16*QT*NW queries of one
 // (batch, head); each wave owns 16*QT queries.  Key/value tiles of KTILE rows
@@ -35,6 +36,64 @@ namespace mpk {
 // The running max (log2 units) is raised only when a tile exceeds it by more than this.
 constexpr float kRescaleLog2 = 8.0f;
 constexpr float kRescaleWeight = 256.0f;  // 2^kRescaleLog2: a weight 2^(s*c - m) above it calls for a raise
+
+// FP32 inputs.  FP16 holds magnitudes of about 6e-5 .. 65504 only, where TF32 (the
+// reference's FP32 kernel) keeps FP32's exponent range.  Attention is exactly
+// invariant under power-of-two scalings: with q' = q 2^-a (per query row),
+// k' = k 2^-b and v' = v 2^-e (per workgroup, over the keys it reads),
+//   s c = (q' . k') (c 2^(a + b))   and   o = (sum_j p_j v'_j / l) 2^e,
+// so the kernels round q', k', v' to FP16 (the same 11-bit significand as before,
+// and no overflow for any finite input), multiply the raw product by the per-row factor c 2^(a + b) in the
+// FP32 FMA that also subtracts the running max, and scale the output by 2^e.
+// Each exponent puts the largest magnitude it covers in [2^13, 2^14): values down to
+// 2^-27 of it keep FP16's full precision, smaller ones lose bits (subnormal) and
+// those below 2^-38 of it become zero - contributions far below the FP32 rounding
+// of the largest terms of a dot product over at most 256 dims.
+constexpr int kF16TopExp = 13;
+__device__ __forceinline__ int f32_scale_exp(float amax) {
+  if (!(amax > 0.f) || !(amax < INFINITY)) return 0;  // all zero (or non-finite): unscaled
+  int e;
+  (void)frexpf(amax, &e);  // amax = f 2^e, f in [0.5, 1)
+  return e - 1 - kF16TopExp;
+}
+
+// 8 consecutive FP32 values through a buffer resource, times 2^-sexp, rounded to FP16
+__device__ __forceinline__ h8 buffer_load8_scaled(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, int sexp) {
+  typedef float v4 __attribute__((ext_vector_type(4)));
+  const v4 a = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+  const v4 b = __builtin_bit_cast(v4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off + 16, 0, 0));
+  h8 h;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    h[j] = (_Float16)ldexpf(a[j], -sexp);
+    h[4 + j] = (_Float16)ldexpf(b[j], -sexp);
+  }
+  return h;
+}
+
+// Largest |x| over rows [0, rows) x cols (cols % 8 == 0) of an FP32 matrix, reduced over
+// the workgroup (NT threads; red: NT / 64 floats of LDS).  Every thread must call it.
+template <int NT>
+__device__ float wg_absmax(const float* base, int64_t row_stride, int rows, int cols, float* red) {
+  float m = 0.f;
+  const int cpr = cols / 8;
+  for (int c = threadIdx.x; c < rows * cpr; c += NT) {
+    const float* p = base + (int64_t)(c / cpr) * row_stride + (c % cpr) * 8;
+    const float4 x0 = *reinterpret_cast<const float4*>(p);
+    const float4 x1 = *reinterpret_cast<const float4*>(p + 4);
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(x0.x), fabsf(x0.y)), fmaxf(fabsf(x0.z), fabsf(x0.w))));
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(x1.x), fabsf(x1.y)), fmaxf(fabsf(x1.z), fabsf(x1.w))));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) r = fmaxf(r, red[w]);
+  __syncthreads();  // red is reused by the next call
+  return r;
+}
 
 struct AttnArgs {
   const void* q;
@@ -111,18 +170,77 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
   const int qw0 = q0 + wave * 16 * QT;       // first query of this wave
   const int qw_last = qw0 + 16 * QT - 1;     // last query of this wave
 
+  const int kv_end = a.causal ? min(q0 + QB, S) : S;  // keys [0, kv_end) can matter
+  const int ntiles = (kv_end + KTILE - 1) / KTILE;
+
+  // FP32 inputs: power-of-two exponents for K and V over the keys this workgroup reads
+  // (see f32_scale_exp); FP16 inputs are used as they are.
+  constexpr bool F32IN = std::is_same<IT, float>::value;
+  int kexp = 0, vexp = 0;
+  if constexpr (F32IN) {
+    __shared__ float red[NW];
+    kexp = __builtin_amdgcn_readfirstlane(
+        f32_scale_exp(wg_absmax<NT>(reinterpret_cast<const float*>(Kp), a.ks[2], kv_end, HD, red)));
+    vexp = __builtin_amdgcn_readfirstlane(
+        f32_scale_exp(wg_absmax<NT>(reinterpret_cast<const float*>(Vp), a.vs[2], kv_end, HD, red)));
+  }
+
   // ---- Q fragments (B operand of S^T = K Q^T), kept in registers ----
-  // q is pre-multiplied by c = scale*log2(e) in FP32 and split into FP16 hi + lo
-  // (hi + lo = q*c to ~2^-22 relative), so two MFMAs give s*c - m directly in
+  // FP16 inputs: q is pre-multiplied by c = scale*log2(e) in FP32 and split into FP16
+  // hi + lo (hi + lo = q*c to ~2^-22 relative), so two MFMAs give s*c - m directly in
   // the FP32 accumulator (which starts at -m): no per-score scaling FMA, and the
   // exponent argument is more accurate than rounding s*c separately.
+  // FP32 inputs: q' = fp16(q 2^-a) per query row (hi only, exact), and the raw product
+  // becomes s*c - m in one FMA with the row's factor ceff = c 2^(a + kexp).
   constexpr int QK_STEPS = HP >= 32 ? HP / 32 : 1;
   h8 qh[QT][QK_STEPS], ql[QT][QK_STEPS];
   h4 qh16[QT], ql16[QT];
+  float ceff[QT];
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     const int q = qw0 + 16 * t + r;
-    if constexpr (HP == 16) {
+    ceff[t] = a.c;
+    if constexpr (F32IN) {
+      // lane (r, g) holds dims 4g .. 4g+3 (HP 16) or kq*32 + 8g .. +7 of query row q
+      float raw[QK_STEPS][8];
+      float mx = 0.f;
+#pragma unroll
+      for (int kq = 0; kq < QK_STEPS; ++kq)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) raw[kq][j] = 0.f;
+      if (q < S) {
+        const float* src = reinterpret_cast<const float*>(Q) + (int64_t)q * a.qs[2];
+        if constexpr (HP == 16) {
+          if (4 * g < HD) {
+            const float4 x = *reinterpret_cast<const float4*>(src + 4 * g);
+            raw[0][0] = x.x; raw[0][1] = x.y; raw[0][2] = x.z; raw[0][3] = x.w;
+          }
+        } else {
+#pragma unroll
+          for (int kq = 0; kq < QK_STEPS; ++kq) {
+            const float4 x0 = *reinterpret_cast<const float4*>(src + kq * 32 + 8 * g);
+            const float4 x1 = *reinterpret_cast<const float4*>(src + kq * 32 + 8 * g + 4);
+            raw[kq][0] = x0.x; raw[kq][1] = x0.y; raw[kq][2] = x0.z; raw[kq][3] = x0.w;
+            raw[kq][4] = x1.x; raw[kq][5] = x1.y; raw[kq][6] = x1.z; raw[kq][7] = x1.w;
+          }
+        }
+      }
+#pragma unroll
+      for (int kq = 0; kq < QK_STEPS; ++kq)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(raw[kq][j]));
+      const int qexp = f32_scale_exp(max_over_groups(mx));
+      ceff[t] = ldexpf(a.c, qexp + kexp);
+      if constexpr (HP == 16) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qh16[t][j] = (_Float16)ldexpf(raw[0][j], -qexp);
+      } else {
+#pragma unroll
+        for (int kq = 0; kq < QK_STEPS; ++kq)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) qh[t][kq][j] = (_Float16)ldexpf(raw[kq][j], -qexp);
+      }
+    } else if constexpr (HP == 16) {
       float v[4] = {0.f, 0.f, 0.f, 0.f};
       if (q < S && 4 * g < HD) {
         const IT* src = Q + (int64_t)q * a.qs[2] + 4 * g;
@@ -169,9 +287,6 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
     for (int dt = 0; dt < SH::DT; ++dt) oacc[t][dt][0] = oacc[t][dt][1] = zero4();
   }
 
-  const int kv_end = a.causal ? min(q0 + QB, S) : S;  // keys [0, kv_end) can matter
-  const int ntiles = (kv_end + KTILE - 1) / KTILE;
-
   // ---- register prefetch of one K/V tile ----
   // K items: one 16-byte chunk of one key row, stored as-is.  V items: the same
   // chunk of two consecutive keys, stored transposed as 8 dwords (d, key pair),
@@ -191,7 +306,11 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
     for (int i = 0; i < SH::PER_THREAD; ++i) {
       const int c = threadIdx.x + i * NT;
       const int key = c / SH::CPK, col = (c % SH::CPK) * 8;
-      if (c < SH::CHUNKS) kreg[i] = buffer_load8_as_half(kr, key * krow_bytes + col * (uint32_t)sizeof(IT), Kp);
+      if (c < SH::CHUNKS) {
+        const uint32_t off = key * krow_bytes + col * (uint32_t)sizeof(IT);
+        if constexpr (F32IN) kreg[i] = buffer_load8_scaled(kr, off, kexp);
+        else kreg[i] = buffer_load8_as_half(kr, off, Kp);
+      }
     }
 #pragma unroll
     for (int i = 0; i < SH::V_PER_THREAD; ++i) {
@@ -199,8 +318,13 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
       const int kp = c % (KTILE / 2), col = (c / (KTILE / 2)) * 8;
       if (c < SH::VITEMS) {
         const uint32_t off = 2 * kp * vrow_bytes + col * (uint32_t)sizeof(IT);
-        vreg[i][0] = buffer_load8_as_half(vr, off, Vp);
-        vreg[i][1] = buffer_load8_as_half(vr, off + vrow_bytes, Vp);
+        if constexpr (F32IN) {
+          vreg[i][0] = buffer_load8_scaled(vr, off, vexp);
+          vreg[i][1] = buffer_load8_scaled(vr, off + vrow_bytes, vexp);
+        } else {
+          vreg[i][0] = buffer_load8_as_half(vr, off, Vp);
+          vreg[i][1] = buffer_load8_as_half(vr, off + vrow_bytes, Vp);
+        }
       }
     }
     if (threadIdx.x < KTILE) {
@@ -262,7 +386,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
         const int krow = 32 * p + pair_row(r, tt);
 #pragma unroll
         for (int t = 0; t < QT; ++t) {
-          const float c0 = (MAYBE_FRESH && fresh[t]) ? 0.f : -mrow[t];
+          const float c0 = (F32IN || (MAYBE_FRESH && fresh[t])) ? 0.f : -mrow[t];
           sc[p][tt][t] = f4{c0, c0, c0, c0};
         }
         if constexpr (HP == 16) {
@@ -270,7 +394,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 #pragma unroll
           for (int t = 0; t < QT; ++t) {
             sc[p][tt][t] = mfma16(ka, qh16[t], sc[p][tt][t]);
-            sc[p][tt][t] = mfma16(ka, ql16[t], sc[p][tt][t]);
+            if constexpr (!F32IN) sc[p][tt][t] = mfma16(ka, ql16[t], sc[p][tt][t]);
           }
         } else {
 #pragma unroll
@@ -279,8 +403,16 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 #pragma unroll
             for (int t = 0; t < QT; ++t) {
               sc[p][tt][t] = mfma32(ka, qh[t][kq], sc[p][tt][t]);
-              sc[p][tt][t] = mfma32(ka, ql[t][kq], sc[p][tt][t]);
+              if constexpr (!F32IN) sc[p][tt][t] = mfma32(ka, ql[t][kq], sc[p][tt][t]);
             }
+          }
+        }
+        if constexpr (F32IN) {  // raw q' . k' -> s*c - m
+#pragma unroll
+          for (int t = 0; t < QT; ++t) {
+            const float negm = (MAYBE_FRESH && fresh[t]) ? 0.f : -mrow[t];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[p][tt][t][i] = fmaf(sc[p][tt][t][i], ceff[t], negm);
           }
         }
       }
@@ -432,7 +564,8 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
   for (int t = 0; t < QT; ++t) {
     const int q = qw0 + 16 * t + r;
     const float lsum = sum_over_groups(lsum_acc[t][0]);
-    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    if constexpr (F32IN) inv = ldexpf(inv, vexp);  // o = (sum p v') / l * 2^vexp
     if (q >= S) continue;
     OT* dst = O + (int64_t)q * a.os[2];
     if constexpr (HP == 16) {
@@ -482,7 +615,10 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 // A operand (rows 0 and 1 pick the queries i and i + 16 out of the P fragment
 // layout), so l sums exactly the FP16 weights that multiply V.
 template <int HD, int NW, int KTILE, typename IT, typename OT, bool KEYMASK>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HD == 32 && KTILE == 64 ? 4 : 1)))
+// (four waves per SIMD, i.e. at most 128 VGPRs, for FP16 input at head dim 32 with 64-key
+// tiles; FP32 input carries a per-row score factor, one register more, and runs at three)
+__global__ __launch_bounds__(64 * NW) __attribute__((
+    amdgpu_waves_per_eu(HD == 32 && KTILE == 64 && std::is_same<IT, _Float16>::value ? 4 : 1)))
 void attention32_kernel(AttnArgs a) {
   constexpr int NT = 64 * NW;
   using SH = AttnShape<HD, KTILE, NT>;
@@ -549,16 +685,69 @@ void attention32_kernel(AttnArgs a) {
   const int q = qw0 + qi;
   const int trow = kappa32(qi);    // tile row this lane feeds as an A-operand row
 
+  const int kv_end = a.causal ? min(q0 + QB, S) : S;
+  const int ntiles = (kv_end + KTILE - 1) / KTILE;
+
+  // FP32 inputs: power-of-two exponents for K and V over the keys this workgroup reads,
+  // and per query row for q (see f32_scale_exp); FP16 inputs are used as they are.
+  constexpr bool F32IN = std::is_same<IT, float>::value;
+  int kexp = 0, vexp = 0;
+  if constexpr (F32IN) {
+    __shared__ float red[NW];
+    kexp = __builtin_amdgcn_readfirstlane(
+        f32_scale_exp(wg_absmax<NT>(reinterpret_cast<const float*>(Kp), a.ks[2], kv_end, HD, red)));
+    vexp = __builtin_amdgcn_readfirstlane(
+        f32_scale_exp(wg_absmax<NT>(reinterpret_cast<const float*>(Vp), a.vs[2], kv_end, HD, red)));
+  }
+
   // Q fragments (B operand of S^T): query q, head dims 16 st + 8 hf .. +7; negated for a
-  // negative scale, so scores map to the exponent as fma(s, |c|, -m)
-  const float c = fabsf(a.c);
+  // negative scale, so scores map to the exponent as fma(s, |c|, -m).  FP32 inputs: q' =
+  // fp16(q 2^-a) for the row's exponent a, and c becomes |c| 2^(a + kexp).
+  float c = fabsf(a.c);
   const bool neg = a.c < 0.f;
   h8 qf[QS];
+  if constexpr (F32IN) {
+    // two passes over the row (the maximum first, then the scaled conversion), so no
+    // FP32 copy of q stays live across the exponent's cross-lane exchange
+    const float* src = reinterpret_cast<const float*>(Q) + (int64_t)q * a.qs[2] + 8 * hf;
+    auto load8 = [&](int st, float (&x)[8]) {
+      float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+      if (q < S) {
+        x0 = *reinterpret_cast<const float4*>(src + 16 * st);
+        x1 = *reinterpret_cast<const float4*>(src + 16 * st + 4);
+      }
+      x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
+      x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+    };
+    float mx = 0.f;
 #pragma unroll
-  for (int st = 0; st < QS; ++st) {
-    h8 v = q < S ? load8_as_half(Q + (int64_t)q * a.qs[2] + 16 * st + 8 * hf) : zero_h8();
-    if (neg) v = -v;
-    qf[st] = v;
+    for (int st = 0; st < QS; ++st) {
+      float x[8];
+      load8(st, x);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(x[j]));
+    }
+    // lanes qi and qi + 32 hold the two halves of query q's head dims
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    const int qexp = f32_scale_exp(fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
+    c = ldexpf(c, qexp + kexp);
+#pragma unroll
+    for (int st = 0; st < QS; ++st) {
+      float x[8];
+      load8(st, x);
+      h8 v;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (_Float16)ldexpf(x[j], -qexp);
+      if (neg) v = -v;
+      qf[st] = v;
+    }
+  } else {
+#pragma unroll
+    for (int st = 0; st < QS; ++st) {
+      h8 v = q < S ? load8_as_half(Q + (int64_t)q * a.qs[2] + 16 * st + 8 * hf) : zero_h8();
+      if (neg) v = -v;
+      qf[st] = v;
+    }
   }
 
   // 0/1 A operand of the row-sum product (16x16x32 layout: lane l holds row l % 16,
@@ -580,9 +769,6 @@ void attention32_kernel(AttnArgs a) {
     for (int e = 0; e < 16; ++e) oacc[dt][e] = 0.f;
   f4 lsum = zero4();    // lanes 0..15: [0] = l of query i, [1] = l of query i + 16
 
-  const int kv_end = a.causal ? min(q0 + QB, S) : S;
-  const int ntiles = (kv_end + KTILE - 1) / KTILE;
-
   // ---- register prefetch / LDS staging of one K/V tile (both row-major) ----
   h8 kreg[SH::PER_THREAD], vreg[SH::PER_THREAD];
   float breg = 0.f;
@@ -600,13 +786,21 @@ void attention32_kernel(AttnArgs a) {
     for (int i = 0; i < SH::PER_THREAD; ++i) {
       const int cc = threadIdx.x + i * NT;
       const int key = cc / SH::CPK, col = (cc % SH::CPK) * 8;
-      if (cc < SH::CHUNKS) kreg[i] = buffer_load8_as_half(kr, key * krow_bytes + col * (uint32_t)sizeof(IT), Kp);
+      if (cc < SH::CHUNKS) {
+        const uint32_t off = key * krow_bytes + col * (uint32_t)sizeof(IT);
+        if constexpr (F32IN) kreg[i] = buffer_load8_scaled(kr, off, kexp);
+        else kreg[i] = buffer_load8_as_half(kr, off, Kp);
+      }
     }
 #pragma unroll
     for (int i = 0; i < SH::PER_THREAD; ++i) {
       const int cc = threadIdx.x + i * NT;
       const int key = cc / SH::CPK, col = (cc % SH::CPK) * 8;
-      if (cc < SH::CHUNKS) vreg[i] = buffer_load8_as_half(vr, key * vrow_bytes + col * (uint32_t)sizeof(IT), Vp);
+      if (cc < SH::CHUNKS) {
+        const uint32_t off = key * vrow_bytes + col * (uint32_t)sizeof(IT);
+        if constexpr (F32IN) vreg[i] = buffer_load8_scaled(vr, off, vexp);
+        else vreg[i] = buffer_load8_as_half(vr, off, Vp);
+      }
     }
     bias_staged = KEYMASK || kb + KTILE > S;
     if (bias_staged && threadIdx.x < KTILE) {
@@ -897,7 +1091,8 @@ void attention32_kernel(AttnArgs a) {
   // ---- normalise and store: lane (i, hf) holds head dims 32 dt + 16 s + 8 hf + j in register 8 s + j ----
   const float a0 = __shfl(lsum[0], qi & 15), a1 = __shfl(lsum[1], qi & 15);
   const float lrow = qi < 16 ? a0 : a1;
-  const float inv = lrow > 0.f ? 1.0f / lrow : 0.f;
+  float inv = lrow > 0.f ? 1.0f / lrow : 0.f;
+  if constexpr (F32IN) inv = ldexpf(inv, vexp);  // o = (sum p v') / l * 2^vexp
   if (q < S) {
     OT* dst = O + (int64_t)q * a.os[2];
 #pragma unroll

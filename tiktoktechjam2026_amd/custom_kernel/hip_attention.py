@@ -11,9 +11,18 @@ projection reads without a transpose.
 
 Differences from the reference, all widening: any sequence length (the
 reference accepts 128 and 1024 only), head_dim in {8, 16, 32, 64, 128, 256}, an
-optional key-padding mask, and FP32 inputs handled by the same FP16-MFMA kernel
-(operands rounded to FP16, i.e. the same 10-bit mantissa the reference's TF32
-dots use).
+optional key-padding mask, and FP32 inputs handled by the same FP16-MFMA kernel.
+
+FP32 inputs.  The reference's FP32 kernel runs its dot products in TF32 (a 10-bit
+mantissa with FP32's 8-bit exponent, ``custom_kernel/triton_attention.py:85,
+105-110``).  FP16 has the same 10-bit mantissa but a 5-bit exponent: normal values
+span about 6.1e-5 .. 65504 only.  So the kernels first scale q (per query row), k
+and v (per workgroup, over the keys it reads) by powers of two that put the largest
+magnitude of each in [2^13, 2^14), round the scaled values to FP16, and undo the
+scales exactly - on the score in the FP32 FMA that subtracts the running max, and on
+the output.  Any finite FP32 input keeps FP16's 11-bit significand: nothing
+overflows, and values down to 2^-27 of their row's (or tile's) largest keep full
+precision.
 """
 
 from __future__ import annotations
