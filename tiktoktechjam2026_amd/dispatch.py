@@ -39,17 +39,32 @@ When the whole layer tail fits one kernel (``LAYER_TAIL_SHAPES``) the forward
 runs 1 + 2L launches: LayerNorm+QKV, then per layer attention and the fused
 tail (out-proj+LN2+FFN+LN1'+QKV', or the final LayerNorm on the last layer).
 
-Tile variants (see the kernel sources for the exact tiles):
-  projections              1: 128x128 (2x2 waves)  2: 128x64  3: 128x32  4: 64x128
+Tile variants (the library's tables, ``mpk_*_auto_variant``, pick among them; see the
+kernel sources for the exact tiles):
+  projections (mpk_linear, mpk_linear_residual)
+                           1: 128x128 (2x2 waves)  2: 128x64  3: 128x32  4: 64x128
                            5: 256x128 double-buffered  6: 256x128 single-buffered
-  out-proj + LN            1: 64 rows/WG           2: 128 rows/WG (d <= 128)
-                           3: 256x256 GEMM tiles, cross-wave LayerNorm (d = 256)
+                           7: 256x256 persistent tiles, 8 waves of 128x64, operands
+                              through registers into LDS
+                           8: as 7 with LDS-DMA operand staging (four-stage ring; FP16 X,
+                              K % 32 == 0, K >= 128; others run 7) - the wide-model choice
+  out-proj + LN (mpk_linear_residual_layernorm)
+                           1: 64 rows/WG           2: 128 rows/WG (row-owning waves, d <= 128)
+                           3: GEMM tiles holding whole rows with a cross-wave LayerNorm
+                              (d 256: 256x256 tiles, 64-wide K chunks; d 512: 128x512, 32-wide)
+  row-wide LayerNorm GEMM (mpk_linear_add_layernorm, d 256 / 512, any K): the variant-3 tiles
   fused FFN + LN           1: 16 rows/wave         2: 32 rows/wave (d <= 256)
-                           3: 32x32-MFMA wide kernel, 128-row workgroups (d = 256)
-  attention                1: 16 queries/wave      2: 32 queries/wave (hd <= 64)
-                           3-5: 128-key tiles / 8-wave workgroups
-                           6-8: 32x32-MFMA kernel (hd 32 and 64)
-  layer tail / LN+QKV      1: 16 rows/wave         2: 32 rows/wave
+                           3: wide kernel, one wave per SIMD (d = 256, FP16 input)
+                           4: role-split wide kernel, a vector and a matrix wave per SIMD
+                              (d = 256) - the built-in choice at d 256
+  attention                16x16-MFMA kernel: 1: 16 queries/wave, 64-key tiles, 4 waves
+                           2: 32 q/wave  3: 32 q/wave, 128-key tiles  4: 32 q/wave, 8 waves
+                           5: 16 q/wave, 128-key tiles
+                           32x32-MFMA kernel (hd 32 and 64, 32 queries/wave):
+                           6: 64-key tiles, 4 waves  7: 64-key tiles, 8 waves
+                           8: 128-key tiles, 4 waves
+  layer tail / LN+QKV      1: 8 waves x 16 rows    2: 8 waves x 32 rows
+                           3: 4 waves x 16 rows (when 128-row tiles would leave CUs idle)
 """
 
 from __future__ import annotations
