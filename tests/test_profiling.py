@@ -109,5 +109,7 @@ def test_parity_table_orders_records(tmp_path):
     ]
     path = tmp_path / "records.json"
     path.write_text(json.dumps(records))
-    lines = profiling.parity_table(str(path)).splitlines()
-    assert lines[2].startswith("| cfg1 | 1 |") and lines[3].startswith("| cfg5 | 0 |")
+    text = profiling.parity_table(str(path), commit="abc1234")
+    assert "Kernels as of commit `abc1234`." in text
+    rows = [ln for ln in text.splitlines() if ln.startswith("| cfg")][1:]  # after the header row
+    assert rows[0].startswith("| cfg1 | 1 |") and rows[1].startswith("| cfg5 | 0 |")
