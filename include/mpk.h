@@ -171,6 +171,34 @@ int mpk_layer_tail(const void* ctx, const float* x, const void* w_o, const void*
 int mpk_layer_tail_supported(int32_t d, int32_t f);
 
 /*
+ * Attention + layer tail in one kernel, for head dim 32 (d == 32 * heads): the causal
+ * (or, with causal == 0, full) attention of every row over this layer's packed QKV, then
+ * everything mpk_layer_tail does, the context never leaving the registers:
+ *   ctx   = attention(qkv_in; heads, scale, causal)   (as mpk_causal_attention, variant 1:
+ *           16x16-MFMA kernel, 64-key tiles - the same arithmetic, bit for bit)
+ *   then x_out, out as mpk_layer_tail with that ctx.
+ * qkv_in: [m, 3d] FP16 = [m / seq_len sequences][seq_len][q | k | v]; m % seq_len == 0 and
+ * seq_len % mpk_attention_layer_tail_rows() == 0, so that every 64-row tile lies in one
+ * sequence; no key mask.  out must not overlap qkv_in (other workgroups read this layer's K
+ * and V while a workgroup writes the next layer's QKV): MPK_EINVAL if it does.  Shapes:
+ * mpk_attention_layer_tail_supported (the layer-tail shapes whose LDS also holds the
+ * attention tiles).  One launch per layer instead of mpk_causal_attention + mpk_layer_tail:
+ * each 64-row workgroup computes its rows' attention itself, so it pays off for short
+ * sequences of narrow models (the module route uses it at d 32 and 64 up to 256 positions,
+ * measured 10-20 % faster per forward; d 128 is built but measured slower than two launches).
+ * Replaces, fused: fp16_causal_attention (custom_kernel/triton_attention.py:341-390) with
+ * the calls mpk_layer_tail replaces; no single reference function corresponds to it.
+ */
+int mpk_attention_layer_tail(const void* qkv_in, const float* x, const void* w_o, const void* b_o,
+                             const float* ln2_w, const float* ln2_b, const void* w_in, const void* b_in,
+                             const void* w_out, const void* b_out, const float* next_ln_w, const float* next_ln_b,
+                             const void* w_qkv, const void* b_qkv, float* x_out, void* out, int last, int64_t m,
+                             int32_t d, int32_t f, int32_t heads, int32_t seq_len, float scale, int causal,
+                             float ln2_eps, float next_ln_eps, void* stream);
+int mpk_attention_layer_tail_supported(int32_t d, int32_t f, int32_t heads);
+int32_t mpk_attention_layer_tail_rows(void);
+
+/*
  * First-layer head: qkv = LayerNorm(x; ln_w, ln_b, eps) w_qkv^T + b_qkv.
  * x: [m, d] FP32; w_qkv: [3d, d] FP16; b_qkv: [3d] FP16; qkv: [m, 3d] FP16.  variant as
  * for mpk_layer_tail.

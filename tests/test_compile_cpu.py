@@ -17,6 +17,14 @@ from tiktoktechjam2026_amd.mixed_precision import MixedPrecisionTransformer
 ROUTES = {
     "layer_tail_d128": (TransformerConfig(2, 64, 128, 4, 128, 2, True),
                         {"mpk.layer_norm_qkv.default": 1, "mpk.attention.default": 2, "mpk.layer_tail.default": 2}),
+    # d_model 64, head dim 32, 64 positions: attention runs inside the layer-tail kernel (1 + L launches)
+    "layer_tail_d64_attention": (TransformerConfig(2, 64, 64, 2, 128, 2, True),
+                                 {"mpk.layer_norm_qkv.default": 1, "mpk.attention_layer_tail.default": 2,
+                                  "mpk.attention.default": 0, "mpk.layer_tail.default": 0}),
+    # 80 positions are not whole 64-row tiles: separate attention + layer tail (1 + 2L launches)
+    "layer_tail_d64_ragged": (TransformerConfig(2, 80, 64, 2, 128, 2, True),
+                              {"mpk.layer_norm_qkv.default": 1, "mpk.attention.default": 2,
+                               "mpk.layer_tail.default": 2}),
     "gemm_ln_epilogue_d256": (TransformerConfig(2, 64, 256, 8, 1024, 2, True),
                               {"mpk.layer_norm.default": 1, "mpk.attention.default": 2}),
     "gemm_d512": (TransformerConfig(2, 64, 512, 8, 2048, 2, True), {"mpk.attention.default": 2}),
@@ -63,7 +71,7 @@ def test_masked_forward_exports_too():
     assert any("masked_fill" in t for t in targets)
 
 
-@pytest.mark.parametrize("name", ["gemm_ln_epilogue_d256", "layer_tail_d128"])
+@pytest.mark.parametrize("name", ["gemm_ln_epilogue_d256", "layer_tail_d128", "layer_tail_d64_attention"])
 def test_forward_with_out_exports_as_one_graph(name):
     """``forward(x, None, out=t)`` (the microbatch harness's direct-write call) traces too."""
     config, expected = ROUTES[name]

@@ -78,6 +78,13 @@ def test_python_tables_match_library(built_library):
         assert bool(lib.mpk_layernorm_qkv_supported(d)) == (d in dispatch.LAYERNORM_QKV_WIDTHS)
         for f in (32, 64, 96, 128, 256, 512, 1024, 2048):
             assert bool(lib.mpk_layer_tail_supported(d, f)) == ((d, f) in dispatch.LAYER_TAIL_SHAPES)
+    # attention inside the layer tail: head dim 32 on the tail shapes, whole 64-row tiles
+    assert lib.mpk_attention_layer_tail_rows() == dispatch.ATTENTION_TAIL_ROWS
+    for d in (16, 32, 64, 96, 128, 256):
+        for f in (32, 64, 96, 128, 256, 512):
+            for heads in (1, 2, 4, 8):
+                expected = (d, f) in dispatch.ATTENTION_TAIL_SHAPES and d == 32 * heads
+                assert bool(lib.mpk_attention_layer_tail_supported(d, f, heads)) == expected, (d, f, heads)
     # the wide fused FFN (variant 4, the role-split kernel) is the library's choice exactly
     # where the route fuses it
     for d in (128, 256, 512):
@@ -124,3 +131,24 @@ def test_copy_weights_packs_qkv():
     assert torch.equal(packed[64:], state["layers.1.attention.v_proj.weight"])
     assert torch.equal(model.state_dict()["layers.1.attention.qkv_proj.bias"][64:],
                        state["layers.1.attention.v_proj.bias"])
+
+
+def test_attention_in_layer_tail_route():
+    """Head dim 32 with d_model 32 or 64 on the layer-tail route runs attention inside the tail
+    for unmasked sequences of whole 64-row tiles up to 256 positions; d_model 128 (measured
+    slower fused), other head dims, masked forwards, ragged or long sequences keep the
+    separate attention kernel."""
+    from tiktoktechjam2026_amd.config import TransformerConfig
+
+    d64 = dispatch.plan(TransformerConfig(2, 128, 64, 2, 128, 2, True))  # hd 32
+    assert d64.fuse_layer_tail and d64.fuse_attention_tail
+    assert dispatch.attention_tail_for(d64, 128, masked=False)
+    assert dispatch.attention_tail_for(d64, 256, masked=False)
+    assert not dispatch.attention_tail_for(d64, 128, masked=True)
+    assert not dispatch.attention_tail_for(d64, 100, masked=False)   # ragged tiles
+    assert not dispatch.attention_tail_for(d64, 512, masked=False)   # long: the attention kernel
+    assert dispatch.plan(TransformerConfig(2, 64, 32, 1, 64, 2, True)).fuse_attention_tail  # D32 H1
+    cfg1 = dispatch.plan(BENCHMARK_CONFIGS["cfg1"])  # D128 H4: hd 32, but d_model 128
+    assert cfg1.fuse_layer_tail and not cfg1.fuse_attention_tail
+    assert not dispatch.plan(BENCHMARK_CONFIGS["cfg3"]).fuse_attention_tail  # D32 H2: hd 16
+    assert not dispatch.plan(TransformerConfig(2, 64, 64, 1, 64, 2, True)).fuse_attention_tail  # hd 64

@@ -89,6 +89,16 @@ SIGNATURES = {
         ],
     ),
     "mpk_layer_tail_supported": (_c_int, [_c_i32, _c_i32]),
+    "mpk_attention_layer_tail": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i32,
+            _c_i32, _c_i32, _c_i32, _c_float, _c_int, _c_float, _c_float, _c_void_p,
+        ],
+    ),
+    "mpk_attention_layer_tail_supported": (_c_int, [_c_i32, _c_i32, _c_i32]),
+    "mpk_attention_layer_tail_rows": (_c_i32, []),
     "mpk_layernorm_qkv": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i32, _c_float, _c_int, _c_void_p],

@@ -389,3 +389,45 @@ def _(ctx, residual, tensors, w_qkv, b_qkv, ln2_eps, next_eps, variant):
     if w_qkv is None:
         return torch.empty_like(residual), ctx.new_empty(ctx.shape, dtype=torch.float32)
     return torch.empty_like(residual), ctx.new_empty((*ctx.shape[:-1], 3 * d), dtype=torch.float16)
+
+
+@torch.library.custom_op("mpk::attention_layer_tail", mutates_args=())
+def attention_layer_tail(
+    qkv: torch.Tensor, residual: torch.Tensor, tensors: List[torch.Tensor], w_qkv: Optional[torch.Tensor],
+    b_qkv: Optional[torch.Tensor], heads: int, scale: float, causal: bool, ln2_eps: float, next_eps: float,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Attention (head dim 32) from this layer's packed ``qkv [B, S, 3D]`` through the next
+    layer's QKV (or the final LayerNorm) in one kernel (``mpk_attention_layer_tail``).
+
+    ``tensors`` as for ``layer_tail``.  Returns ``(residual_out, next qkv FP16 [B, S, 3D])``,
+    or ``(residual_out, normalized FP32)`` when ``w_qkv`` is None (last layer); the next
+    layer's QKV is always a new tensor (the kernel reads ``qkv`` while it writes it).
+    """
+    w_o, b_o, ln2_w, ln2_b, w_in, b_in, w_out, b_out, next_w, next_b = tensors
+    d = residual.shape[-1]
+    f = w_in.shape[0]
+    last = w_qkv is None
+    residual_out = torch.empty_like(residual)
+    shape = residual.shape if last else (*residual.shape[:-1], 3 * d)
+    out = torch.empty(shape, device=qkv.device, dtype=torch.float32 if last else torch.float16)
+    _require_aligned("unsupported fused attention layer-tail inputs", qkv, residual, *tensors, w_qkv, b_qkv,
+                     residual_out, out)
+    _lib.check(
+        _lib.load().mpk_attention_layer_tail(
+            qkv.data_ptr(), residual.data_ptr(), w_o.data_ptr(), b_o.data_ptr(), ln2_w.data_ptr(),
+            ln2_b.data_ptr(), w_in.data_ptr(), b_in.data_ptr(), w_out.data_ptr(), b_out.data_ptr(),
+            next_w.data_ptr(), next_b.data_ptr(), _ptr(w_qkv), _ptr(b_qkv), residual_out.data_ptr(),
+            out.data_ptr(), 1 if last else 0, _rows(residual, d), d, f, int(heads), int(residual.shape[-2]),
+            float(scale), 1 if causal else 0, float(ln2_eps), float(next_eps), _lib.stream_handle(qkv.device),
+        ),
+        "mpk_attention_layer_tail",
+    )
+    return residual_out, out
+
+
+@attention_layer_tail.register_fake
+def _(qkv, residual, tensors, w_qkv, b_qkv, heads, scale, causal, ln2_eps, next_eps):
+    d = residual.shape[-1]
+    if w_qkv is None:
+        return torch.empty_like(residual), residual.new_empty(residual.shape, dtype=torch.float32)
+    return torch.empty_like(residual), residual.new_empty((*residual.shape[:-1], 3 * d), dtype=torch.float16)

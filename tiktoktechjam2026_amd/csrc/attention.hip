@@ -33,8 +33,7 @@
 
 namespace mpk {
 
-// The running max (log2 units) is raised only when a tile exceeds it by more than this.
-constexpr float kRescaleLog2 = 8.0f;
+// (kRescaleLog2, the lazy-raise threshold of the running max, is in mpk_common.h)
 constexpr float kRescaleWeight = 256.0f;  // 2^kRescaleLog2: a weight 2^(s*c - m) above it calls for a raise
 
 // FP32 inputs.  FP16 holds magnitudes of about 6e-5 .. 65504 only, where TF32 (the

@@ -53,6 +53,12 @@ struct TailArgs {
   int64_t m;
   int f;
   float eps2, eps1;
+  // attention stage (mpk_attention_layer_tail only): this layer's packed QKV [m, 3d] FP16
+  // (read, never written: the kernel writes the next layer's into `out`), the sequence
+  // length, causality and scale * log2(e)
+  const _Float16* qkv_in;
+  int seq, causal;
+  float attn_c;
 };
 
 constexpr int kLdsBudget = 160 * 1024;
@@ -71,7 +77,9 @@ enum QkvMode : int { kQkvLds = 1, kQkvReg = 2 };
 // multiple of 16 bytes (measured with SQ_LDS_BANK_CONFLICT).  D + 16 and F + 16 halves are
 // odd multiples of 32 bytes for every supported width (multiples of 32).  Weight rows are
 // stored at LDS row w_slot(row), so the 16 rows of a fragment are consecutive.
-template <int D, int F, int TM, bool STAGE1, bool QKV, int QMODE, int W>
+// ATTN (the fused attention + tail kernel): the parameters follow the weights and the
+// attention stage's tiles overlay the QKV row ring, which is idle while attention runs.
+template <int D, int F, int TM, bool STAGE1, bool QKV, int QMODE, int W, bool ATTN = false>
 struct TailShape {
   static constexpr int LDD = D + 16;  // row stride of [*, D] tiles (halves)
   static constexpr int LDF = F + 16;  // row stride of Wout [D, F] (halves)
@@ -93,8 +101,11 @@ struct TailShape {
   static constexpr int P_BE1 = P_G1 + D;
   static constexpr int P_BQKV = P_BE1 + D;
   static constexpr int NPARAM = P_BQKV + (QKV ? 3 * D : 0);
-  static constexpr int PARAM_OFF = (TOTAL + 7) / 8 * 8;  // halves; 16-byte aligned
-  static constexpr int BYTES = PARAM_OFF * 2 + NPARAM * 4;
+  static constexpr int RING_HALVES = TOTAL - NBUF;                                 // QKV row ring
+  static constexpr int PARAM_OFF = ((ATTN ? NBUF : TOTAL) + 7) / 8 * 8;            // halves; 16-byte aligned
+  static constexpr int RING = ATTN ? PARAM_OFF + (2 * NPARAM + 7) / 8 * 8 : NBUF;  // halves
+  static constexpr int BYTES = ATTN ? (RING + RING_HALVES) * 2 : PARAM_OFF * 2 + NPARAM * 4;
+  static constexpr int ATT_OFF_BYTES = RING * 2;  // the attention tiles (ATTN only)
 };
 
 // Two-phase staging of a [ROWS, COLS] FP16 matrix into LDS (row stride LD, row j at
@@ -177,7 +188,7 @@ struct TileIn {
   float x[TM][D / 32][8];
 };
 
-template <int D, int TM, bool STAGE1>
+template <int D, int TM, bool STAGE1, bool LOAD_CTX = STAGE1>
 __device__ __forceinline__ void load_tile(TileIn<D, TM, STAGE1>& in, const TailArgs& a, int64_t m0, int r, int g) {
   constexpr int PN = D / 32;
   typedef float v4 __attribute__((ext_vector_type(4)));
@@ -187,7 +198,7 @@ __device__ __forceinline__ void load_tile(TileIn<D, TM, STAGE1>& in, const TailA
 #pragma unroll
   for (int t = 0; t < TM; ++t) {
     const uint32_t row = (uint32_t)(16 * t + r);
-    if constexpr (STAGE1) {
+    if constexpr (STAGE1 && LOAD_CTX) {
       const __amdgpu_buffer_rsrc_t crs = make_rsrc(a.ctx + m0 * D, rows * (uint32_t)(D * 2));
 #pragma unroll
       for (int ks = 0; ks < PN; ++ks)
@@ -207,11 +218,355 @@ __device__ __forceinline__ void load_tile(TileIn<D, TM, STAGE1>& in, const TailA
   }
 }
 
-template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE, int W>
+// ---- attention stage (head dim 32) of the fused attention + layer-tail kernel ----
+// The context of a wave's 16 TM rows, computed in the kernel instead of read from HBM: per
+// head, the arithmetic of attention_kernel<32, TM, 64, W, FP16 in/out, no key mask>
+// (attention.hip) - q c split into FP16 hi + lo, S^T = K (q c)^T - m on 16x16x32 MFMAs
+// (the accumulator starts at -m), a running max raised lazily (by more than kRescaleLog2
+// only), p = exp2(.) rounded to FP16, l and O^T = V^T P^T by MFMAs, o = O / l - over the
+// same 64-key tiles, so the context is bit-identical to that kernel's.  Lane (r, g) ends
+// with dims 8g .. 8g + 7 of head h of row 16 t + r: exactly the B-operand fragment
+// ctx[t][h] that the out-projection's k-step h reads.  All rows of the workgroup lie in
+// one sequence (the launcher checks seq % rows == 0).
+// A step is one 64-key tile of every head: the workgroup's rows are few (64), so a step per
+// (head, tile) would leave each step bound by a memory latency; a step per tile exposes one
+// latency per tile at most.  The tiles go through NB LDS buffers (2 where they fit beside
+// the weights, else 1 with the next tile held in registers across the step).
+constexpr int kAttnKT = 64;                     // keys per tile
+constexpr int kAttnLDK = 40;                    // K tile row stride (halves; 16-byte padded)
+constexpr int kAttnLDV = kAttnKT + 8;           // V^T tile row stride (halves)
+constexpr int kAttnKBuf = kAttnKT * kAttnLDK;   // halves per K tile of one head
+constexpr int kAttnVBuf = 32 * kAttnLDV;        // halves per V^T tile of one head
+// bytes of one buffer: K and V^T tiles of every head, then the key bias [KT] (floats)
+template <int D>
+constexpr int attn_buf_bytes() { return (D / 32) * (kAttnKBuf + kAttnVBuf) * 2 + kAttnKT * 4; }
+
+// Registers of the attention stage's global reads: one K / V tile of every head with its
+// key bias, and the wave's raw queries.  The queries are read (and split) before the first
+// tile is requested; issuing the first tile's reads earlier, ahead of the weight prologue,
+// measured slower at d_model 128 (registers held across the prologue push the
+// register-resident QKV weights into AGPRs).
+template <int D, int TM, int W>
+struct AttnRegs {
+  static constexpr int H = D / 32;
+  static constexpr int NT = 64 * W;
+  static constexpr int KT = kAttnKT;
+  static constexpr int CPR = D / 8;                    // 16-byte chunks of a key's K (or V) row
+  static constexpr int CHUNKS = KT * CPR;              // K tile: one chunk per item
+  static constexpr int PER_THREAD = (CHUNKS + NT - 1) / NT;
+  static constexpr int VITEMS = (KT / 2) * CPR;        // V tile: a key pair x one chunk per item
+  static constexpr int V_PER_THREAD = (VITEMS + NT - 1) / NT;
+  static constexpr int U = H * TM;                     // row tiles u = h TM + t
+  h8 kreg[PER_THREAD], vreg[V_PER_THREAD][2], qraw[U];
+  float breg;
+
+  // K and V rows kb .. kb + KT - 1 of every head of the sequence at seq (S positions)
+  __device__ __forceinline__ void fetch(const _Float16* seq, int S, int kb) {
+    const uint32_t row_bytes = (uint32_t)(3 * D * 2);
+    const _Float16* Kp = seq + (int64_t)kb * (3 * D) + D;
+    const _Float16* Vp = Kp + D;
+    const uint32_t rows = (uint32_t)min(KT, S - kb);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(Kp, rows * row_bytes);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(Vp, rows * row_bytes);
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int cc = threadIdx.x + i * NT;
+      const int key = cc / CPR, col = (cc % CPR) * 8;
+      if (cc < CHUNKS) kreg[i] = buffer_load8_as_half(kr, key * row_bytes + col * 2u, Kp);
+    }
+#pragma unroll
+    for (int i = 0; i < V_PER_THREAD; ++i) {
+      const int cc = threadIdx.x + i * NT;
+      const int kp = cc % (KT / 2), col = (cc / (KT / 2)) * 8;
+      if (cc < VITEMS) {
+        const uint32_t off = 2 * kp * row_bytes + col * 2u;
+        vreg[i][0] = buffer_load8_as_half(vr, off, Vp);
+        vreg[i][1] = buffer_load8_as_half(vr, off + row_bytes, Vp);
+      }
+    }
+    breg = kb + (int)threadIdx.x < S ? 0.f : -INFINITY;
+  }
+  // lane (r, g): query row qw0 + 16 t + r, dims 8g .. 8g + 7 of head h, for u = h TM + t
+  __device__ __forceinline__ void load_q(const _Float16* seq, int S, int qw0, int r, int g) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int q = qw0 + 16 * (u % TM) + r;
+      qraw[u] = q < S ? *reinterpret_cast<const h8*>(seq + (int64_t)q * (3 * D) + 32 * (u / TM) + 8 * g) : zero_h8();
+    }
+  }
+};
+
+template <int D, int TM, int W, int NB>
+__device__ __forceinline__ void tail_attention(const TailArgs& a, unsigned char* att_lds, int64_t wg0,
+                                               h8 (&ctx)[TM][D / 32]) {
+  static_assert(NB == 1 || NB == 2, "one or two tile buffers");
+  constexpr int H = D / 32;
+  constexpr int NT = 64 * W;
+  constexpr int ROWS = 16 * TM * W;
+  constexpr int KT = kAttnKT;
+  constexpr int NP = KT / 32;                          // key pairs per tile
+  using R = AttnRegs<D, TM, W>;
+  R st;
+  constexpr int CPR = R::CPR, CHUNKS = R::CHUNKS, PER_THREAD = R::PER_THREAD;
+  constexpr int VITEMS = R::VITEMS, V_PER_THREAD = R::V_PER_THREAD;
+  constexpr int BUF = attn_buf_bytes<D>();
+  auto ks_of = [&](int buf, int h) {
+    return reinterpret_cast<_Float16*>(att_lds + buf * BUF) + h * kAttnKBuf;
+  };
+  auto vt_of = [&](int buf, int h) {
+    return reinterpret_cast<_Float16*>(att_lds + buf * BUF) + H * kAttnKBuf + h * kAttnVBuf;
+  };
+  auto kbias_of = [&](int buf) {
+    return reinterpret_cast<float*>(reinterpret_cast<_Float16*>(att_lds + buf * BUF) + H * (kAttnKBuf + kAttnVBuf));
+  };
+
+  const int S = a.seq;
+  const int64_t bseq = wg0 / S;
+  const int pos0 = (int)(wg0 - bseq * S);              // the workgroup's first position
+  const int l = threadIdx.x & 63, wave = wave_id();
+  const int r = l & 15, g = l >> 4;
+  const int qw0 = pos0 + wave * 16 * TM;               // first query of this wave
+  const int qw_last = qw0 + 16 * TM - 1;
+  const int kv_end = a.causal ? min(pos0 + ROWS, S) : S;
+  const int ntiles = (kv_end + KT - 1) / KT;
+  const _Float16* seq = a.qkv_in + bseq * (int64_t)S * (3 * D);
+  const float c = a.attn_c;
+
+  h8 ones_row;  // row 0 of the row-sum product's A operand: all ones
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones_row[j] = r == 0 ? (_Float16)1.0f : (_Float16)0.0f;
+
+  auto stash = [&](int buf) {  // K row-major and V transposed, per head
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int cc = threadIdx.x + i * NT;
+      if (cc < CHUNKS) {
+        const int key = cc / CPR, col = (cc % CPR) * 8;
+        *reinterpret_cast<h8*>(&ks_of(buf, col / 32)[key * kAttnLDK + col % 32]) = st.kreg[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < V_PER_THREAD; ++i) {
+      const int cc = threadIdx.x + i * NT;
+      if (cc < VITEMS) {
+        const int kp = cc % (KT / 2), col = (cc / (KT / 2)) * 8;
+        _Float16* vt = vt_of(buf, col / 32);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+          h2 pair;
+          pair[0] = st.vreg[i][0][j];
+          pair[1] = st.vreg[i][1][j];
+          *reinterpret_cast<h2*>(&vt[(col % 32 + j) * kAttnLDV + 2 * kp]) = pair;
+        }
+      }
+    }
+    if (threadIdx.x < KT) kbias_of(buf)[threadIdx.x] = st.breg;
+  };
+
+  // Row tiles u = h TM + t (head h, rows 16 t ..): every step below runs over all of them,
+  // so a wave has H TM independent chains (it is alone on its SIMD at these sizes).
+  constexpr int U = H * TM;
+  // q c in FP32, split into FP16 hi + lo (lane (r, g): query row 16 t + r, dims 8g .. 8g + 7 of head h)
+  st.load_q(seq, S, qw0, r, g);
+  h8 qh[U], ql[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = (float)st.qraw[u][j] * c;
+      qh[u][j] = (_Float16)v;
+      ql[u][j] = (_Float16)(v - (float)qh[u][j]);
+    }
+  }
+  float mrow[U];
+  bool fresh[U];
+  f4 oacc[U][2], lsum_acc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    mrow[u] = 0.f;
+    fresh[u] = true;
+    lsum_acc[u] = zero4();
+    oacc[u][0] = oacc[u][1] = zero4();
+  }
+
+  // one key tile of every head: S^T, online softmax, O^T += V^T P^T (attention_kernel's process, hd 32)
+  auto process_all = [&](const int kb, const int buf, auto first_tag) {
+    constexpr bool MAYBE_FRESH = decltype(first_tag)::value;
+    if (a.causal && kb > qw_last) return;  // whole tile is in this wave's future
+    const float* kbb = kbias_of(buf);
+    const int npv = a.causal ? min(NP, (qw_last - kb) / 32 + 1) : NP;
+    const bool need_causal = a.causal && kb + 32 * npv - 1 > qw0;
+    const bool need_bias = kb + KT > S;
+    f4 sc[NP][2][U];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      if (p >= npv) break;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int krow = 32 * p + pair_row(r, tt);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float c0 = (MAYBE_FRESH && fresh[u]) ? 0.f : -mrow[u];
+          sc[p][tt][u] = f4{c0, c0, c0, c0};
+        }
+        h8 ka[H];
+#pragma unroll
+        for (int h = 0; h < H; ++h) ka[h] = *reinterpret_cast<const h8*>(&ks_of(buf, h)[krow * kAttnLDK + 8 * g]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          sc[p][tt][u] = mfma32(ka[u / TM], qh[u], sc[p][tt][u]);
+          sc[p][tt][u] = mfma32(ka[u / TM], ql[u], sc[p][tt][u]);
+        }
+      }
+    }
+    if (need_causal) {
+      const int pl = npv - 1;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int lim = qw0 + 16 * (u % TM) + r - kb - 32 * pl - 8 * g;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          if (p != pl) continue;
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (4 * tt + i > lim) sc[p][tt][u][i] = -INFINITY;
+        }
+      }
+    }
+    if (need_bias) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        if (p >= npv) break;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[p][tt][u][i] += kbb[32 * p + 8 * g + 4 * tt + i];
+      }
+    }
+    float pm[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float mx = sc[0][0][u][0];
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        if (p >= npv) break;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[p][tt][u][i]);
+      }
+      pm[u] = mx;
+    }
+    // a row tile that needs no shift gets shift 0 below (x - 0 == x), so testing every head
+    // at once leaves each head's arithmetic as attention_kernel's
+    bool any_shift = false;
+#pragma unroll
+    for (int u = 0; u < U; ++u) any_shift |= (MAYBE_FRESH && fresh[u]) || pm[u] > kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(any_shift)) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float mx = max_over_groups(pm[u]);
+        const bool is_fresh = MAYBE_FRESH && fresh[u];
+        const bool shift_row = is_fresh ? (mx > -INFINITY) : (mx > kRescaleLog2);
+        const float shift = shift_row ? mx : 0.f;
+        if (shift_row && !is_fresh) {
+          const float alpha = __builtin_amdgcn_exp2f(-shift);
+          lsum_acc[u] *= alpha;
+          oacc[u][0] *= alpha;
+          oacc[u][1] *= alpha;
+        }
+        if (shift_row) {
+          mrow[u] = is_fresh ? shift : mrow[u] + shift;
+          fresh[u] = false;
+        }
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          if (p >= npv) break;
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[p][tt][u][i] -= shift;
+        }
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      if (p >= npv) break;
+      h8 pf[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pf[u][4 * tt + i] = (_Float16)__builtin_amdgcn_exp2f(sc[p][tt][u][i]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) lsum_acc[u] = mfma32(ones_row, pf[u], lsum_acc[u]);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int drow = pair_row(r, tt);
+        h8 va[H];
+#pragma unroll
+        for (int h = 0; h < H; ++h) va[h] = *reinterpret_cast<const h8*>(&vt_of(buf, h)[drow * kAttnLDV + 32 * p + 8 * g]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) oacc[u][tt] = mfma32(va[u / TM], pf[u], oacc[u][tt]);
+      }
+    }
+  };
+
+  st.fetch(seq, S, 0);
+  __syncthreads();
+  stash(0);
+  __syncthreads();
+  for (int tile = 0; tile < ntiles; ++tile) {
+    const bool more = tile + 1 < ntiles;
+    const int buf = NB == 2 ? (tile & 1) : 0;
+    if (more) st.fetch(seq, S, (tile + 1) * KT);
+    if (tile == 0)
+      process_all(0, buf, std::true_type{});
+    else
+      process_all(tile * KT, buf, std::false_type{});
+    if (more) {
+      if constexpr (NB == 1) __syncthreads();  // every wave is done with the buffer
+      stash(NB == 2 ? buf ^ 1 : 0);
+    }
+    __syncthreads();  // the stashed tile is visible; the last one also frees the area
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const float lsum = sum_over_groups(lsum_acc[u][0]);
+    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ctx[u % TM][u / TM][i] = (_Float16)(oacc[u][0][i] * inv);
+      ctx[u % TM][u / TM][4 + i] = (_Float16)(oacc[u][1][i] * inv);
+    }
+  }
+}
+
+// LDS of the fused kernel: two attention buffers where they fit, else one
+template <int D, int F, int TM, bool QKV, int QMODE, int W>
+constexpr int attn_nbuf() {
+  using SH = TailShape<D, F, TM, true, QKV, QMODE, W, true>;
+  return SH::ATT_OFF_BYTES + 2 * attn_buf_bytes<D>() <= kLdsBudget ? 2 : 1;
+}
+template <int D, int F, int TM, bool QKV, int QMODE, int W>
+constexpr int attn_lds_bytes() {
+  using SH = TailShape<D, F, TM, true, QKV, QMODE, W, true>;
+  constexpr int att = SH::ATT_OFF_BYTES + attn_nbuf<D, F, TM, QKV, QMODE, W>() * attn_buf_bytes<D>();
+  return att > SH::BYTES ? att : SH::BYTES;
+}
+
+template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE, int W, bool ATTN = false>
 __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
+  static_assert(!ATTN || STAGE1, "the attention stage feeds the out-projection");
   constexpr bool QKV = !LAST;
   constexpr int NT = 64 * W;
-  using SH = TailShape<D, F, TM, STAGE1, QKV, QMODE, W>;
+  using SH = TailShape<D, F, TM, STAGE1, QKV, QMODE, W, ATTN>;
   constexpr int PN = D / 32;   // feature pairs of a D-wide row
   constexpr int KS = D / 32;   // k-steps over D
   constexpr int FQ = F / 32;   // hidden feature pairs
@@ -284,11 +639,15 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
 
   int64_t tile = blockIdx.x;
   TileIn<D, TM, STAGE1> cur;
-  load_tile<D, TM, STAGE1>(cur, a, tile * ROWS + wave * 16 * TM, r, g);
+  load_tile<D, TM, STAGE1, !ATTN>(cur, a, tile * ROWS + wave * 16 * TM, r, g);
 
   for (; tile < ntiles; tile += gridDim.x) {
     const int64_t wg0 = tile * ROWS;
     const int64_t m0 = wg0 + wave * 16 * TM;
+    if constexpr (ATTN) {
+      tail_attention<D, TM, W, attn_nbuf<D, F, TM, QKV, QMODE, W>()>(
+          a, reinterpret_cast<unsigned char*>(lds) + SH::ATT_OFF_BYTES, wg0, cur.ctx);
+    }
     // rows of this wave / workgroup that exist (stores to the others are dropped by the buffer resource)
     const uint32_t wrows = (uint32_t)(M - m0 <= 0 ? 0 : (M - m0 < 16 * TM ? M - m0 : 16 * TM));
     const uint32_t grows = (uint32_t)(M - wg0 < ROWS ? M - wg0 : ROWS);
@@ -463,7 +822,8 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
     // are dead, so that their 48+ registers are not held through the
     // out-projection and FFN stages; the QKV stage still covers the load latency.
     TileIn<D, TM, STAGE1> nxt;
-    if (tile + gridDim.x < ntiles) load_tile<D, TM, STAGE1>(nxt, a, (tile + gridDim.x) * ROWS + wave * 16 * TM, r, g);
+    if (tile + gridDim.x < ntiles)
+      load_tile<D, TM, STAGE1, !ATTN>(nxt, a, (tile + gridDim.x) * ROWS + wave * 16 * TM, r, g);
 
     if constexpr (QKV && QMODE == kQkvLds) {
       _Float16* qkv = static_cast<_Float16*>(a.out);
@@ -500,7 +860,7 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
 
     if constexpr (QKV && QMODE == kQkvReg) {
       // publish this wave's normalized rows, then project all workgroup rows onto this wave's columns
-      _Float16* nbuf = lds + SH::NBUF;
+      _Float16* nbuf = lds + SH::RING;
 #pragma unroll
       for (int t = 0; t < TM; ++t)
 #pragma unroll
@@ -555,12 +915,12 @@ static int tail_cu_count() {
   return cached[dev];
 }
 
-template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE, int W>
+template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE, int W, bool ATTN = false>
 static hipError_t launch_tail(const TailArgs& a, hipStream_t s) {
-  using SH = TailShape<D, F, TM, STAGE1, !LAST, QMODE, W>;
-  constexpr int lds_bytes = SH::BYTES;
+  constexpr int lds_bytes = ATTN ? attn_lds_bytes<D, F, TM, !LAST, QMODE, W>()
+                                 : TailShape<D, F, TM, STAGE1, !LAST, QMODE, W>::BYTES;
   static_assert(lds_bytes <= kLdsBudget, "weights exceed LDS");
-  auto kern = layer_tail_kernel<D, F, TM, STAGE1, LAST, QMODE, W>;
+  auto kern = layer_tail_kernel<D, F, TM, STAGE1, LAST, QMODE, W, ATTN>;
   if (lds_bytes > 64 * 1024) {
     static std::atomic<bool> attribute_set{false};  // once per instantiation
     if (!attribute_set.load(std::memory_order_acquire)) {
@@ -602,6 +962,26 @@ static hipError_t tail_variant(int variant, bool last, const TailArgs& a, hipStr
 
 // 64-row tiles when 128-row tiles would not give every CU one
 static int tail_auto_variant(int64_t m) { return (m + 127) / 128 < tail_cu_count() ? 3 : 1; }
+
+// Fused attention + tail: 4 waves x 16 rows (64-row tiles; a tile's rows lie in one
+// sequence when seq % 64 == 0), where the weights, parameters and the attention area fit.
+constexpr int kAttnTailRows = 64;
+template <int D, int F>
+constexpr bool attn_tail_fits() {
+  constexpr int QM = qkv_mode<D, F, true>();
+  return (QM != kQkvReg || (3 * D) % (16 * 4) == 0) &&
+         attn_lds_bytes<D, F, 1, true, QM, 4>() <= kLdsBudget;
+}
+template <int D, int F>
+static hipError_t attn_tail_launch(bool last, const TailArgs& a, hipStream_t s) {
+  if constexpr (attn_tail_fits<D, F>()) {
+    constexpr int QM = qkv_mode<D, F, true>();
+    return last ? launch_tail<D, F, 1, true, true, QM, 4, true>(a, s) : launch_tail<D, F, 1, true, false, QM, 4, true>(a, s);
+  } else {
+    (void)last; (void)a; (void)s;
+    return (hipError_t)MPK_EUNSUPPORTED;
+  }
+}
 
 }  // namespace mpk
 
@@ -649,6 +1029,68 @@ extern "C" int mpk_layer_tail(const void* ctx, const float* x, const void* w_o, 
   else if (d == 64 && f == 128) e = tail_variant<64, 128, true>(variant, L, a, s);
   else if (d == 64 && f == 256) e = tail_variant<64, 256, true>(variant, L, a, s);
   else e = tail_variant<128, 128, true>(variant, L, a, s);
+  return (int)e;
+}
+
+extern "C" int mpk_attention_layer_tail_supported(int32_t d, int32_t f, int32_t heads) {
+  if (!mpk_layer_tail_supported(d, f) || heads <= 0 || d != 32 * heads) return 0;
+  if (d == 32 && f == 32) return attn_tail_fits<32, 32>();
+  if (d == 32 && f == 64) return attn_tail_fits<32, 64>();
+  if (d == 32 && f == 128) return attn_tail_fits<32, 128>();
+  if (d == 64 && f == 64) return attn_tail_fits<64, 64>();
+  if (d == 64 && f == 128) return attn_tail_fits<64, 128>();
+  if (d == 64 && f == 256) return attn_tail_fits<64, 256>();
+  return attn_tail_fits<128, 128>();
+}
+
+extern "C" int32_t mpk_attention_layer_tail_rows(void) { return kAttnTailRows; }
+
+extern "C" int mpk_attention_layer_tail(const void* qkv_in, const float* x, const void* w_o, const void* b_o,
+                                        const float* ln2_w, const float* ln2_b, const void* w_in, const void* b_in,
+                                        const void* w_out, const void* b_out, const float* next_ln_w,
+                                        const float* next_ln_b, const void* w_qkv, const void* b_qkv, float* x_out,
+                                        void* out, int last, int64_t m, int32_t d, int32_t f, int32_t heads,
+                                        int32_t seq_len, float scale, int causal, float ln2_eps, float next_ln_eps,
+                                        void* stream) {
+  if (!qkv_in || !x || !w_o || !b_o || !ln2_w || !ln2_b || !w_in || !b_in || !w_out || !b_out || !next_ln_w ||
+      !next_ln_b || !x_out || !out || m < 0 || seq_len <= 0)
+    return MPK_EINVAL;
+  if (!last && (!w_qkv || !b_qkv)) return MPK_EINVAL;
+  if (!mpk_attention_layer_tail_supported(d, f, heads)) return MPK_EUNSUPPORTED;
+  if (seq_len % kAttnTailRows != 0 || m % seq_len != 0) return MPK_EUNSUPPORTED;
+  const void* ptrs[] = {qkv_in, x, w_o, b_o, ln2_w, ln2_b, w_in, b_in, w_out, b_out, next_ln_w, next_ln_b, x_out, out};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return MPK_EALIGN;
+  if (!last && (!aligned16(w_qkv) || !aligned16(b_qkv))) return MPK_EALIGN;
+  // other workgroups read this layer's K and V while a workgroup writes its rows of the
+  // next layer's QKV: the two buffers must not overlap
+  {
+    const uintptr_t in0 = reinterpret_cast<uintptr_t>(qkv_in), in1 = in0 + (uintptr_t)m * 3 * d * 2;
+    const uintptr_t o0 = reinterpret_cast<uintptr_t>(out);
+    const uintptr_t o1 = o0 + (uintptr_t)m * (last ? d * 4 : 3 * d * 2);
+    if (m > 0 && in0 < o1 && o0 < in1) return MPK_EINVAL;
+  }
+  if (m == 0) return MPK_OK;
+  TailArgs a{};
+  a.wo = static_cast<const _Float16*>(w_o); a.bo = static_cast<const _Float16*>(b_o); a.g2 = ln2_w; a.be2 = ln2_b;
+  a.x = x;
+  a.win = static_cast<const _Float16*>(w_in); a.bin = static_cast<const _Float16*>(b_in);
+  a.wout = static_cast<const _Float16*>(w_out); a.bout = static_cast<const _Float16*>(b_out);
+  a.g1 = next_ln_w; a.be1 = next_ln_b;
+  a.wqkv = static_cast<const _Float16*>(w_qkv); a.bqkv = static_cast<const _Float16*>(b_qkv);
+  a.x_out = x_out; a.out = out; a.m = m; a.f = f; a.eps2 = ln2_eps; a.eps1 = next_ln_eps;
+  a.qkv_in = static_cast<const _Float16*>(qkv_in);
+  a.seq = seq_len; a.causal = causal ? 1 : 0; a.attn_c = scale * 1.4426950408889634f;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool L = last != 0;
+  hipError_t e;
+  if (d == 32 && f == 32) e = attn_tail_launch<32, 32>(L, a, s);
+  else if (d == 32 && f == 64) e = attn_tail_launch<32, 64>(L, a, s);
+  else if (d == 32 && f == 128) e = attn_tail_launch<32, 128>(L, a, s);
+  else if (d == 64 && f == 64) e = attn_tail_launch<64, 64>(L, a, s);
+  else if (d == 64 && f == 128) e = attn_tail_launch<64, 128>(L, a, s);
+  else if (d == 64 && f == 256) e = attn_tail_launch<64, 256>(L, a, s);
+  else e = attn_tail_launch<128, 128>(L, a, s);
   return (int)e;
 }
 

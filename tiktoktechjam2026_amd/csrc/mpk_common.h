@@ -242,6 +242,10 @@ __device__ __forceinline__ float max_over_groups(float v) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// Flash attention's running row max (log2 units) is raised only when a tile exceeds it by
+// more than this (attention.hip, and the attention stage of layer_tail.hip).
+constexpr float kRescaleLog2 = 8.0f;
+
 // ---- LDS-DMA copies (global -> LDS without registers) ----
 typedef __attribute__((address_space(3))) void lds_void;
 

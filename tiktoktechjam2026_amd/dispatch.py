@@ -80,6 +80,19 @@ ATTENTION_HEAD_DIMS = (8, 16, 32, 64, 128, 256)
 # must equal mpk_layer_tail_supported / mpk_layernorm_qkv_supported in the library.
 LAYER_TAIL_SHAPES = frozenset({(32, 32), (32, 64), (32, 128), (64, 64), (64, 128), (64, 256), (128, 128)})
 LAYERNORM_QKV_WIDTHS = frozenset({32, 64, 128})
+# Attention inside the layer-tail kernel (head dim 32; must equal
+# mpk_attention_layer_tail_supported): one launch per layer for short sequences made of whole
+# 64-row tiles, without a key mask.
+ATTENTION_TAIL_SHAPES = frozenset(s for s in LAYER_TAIL_SHAPES if s[0] % 32 == 0)
+ATTENTION_TAIL_ROWS = 64
+# Where the route uses it (whole forwards, HIP-graph replay on MI355X, fused vs separate
+# attention + tail): d_model 32 is 18-20 % faster up to 256 positions, d_model 64 10-17 %;
+# at 512 positions d_model 64 is 40 % slower (a workgroup's 64 rows then walk 8 key tiles
+# with one wave per SIMD, where the attention kernel spreads them over many CUs), and
+# d_model 128 is slower at every length (2-4 % at 128 positions: its register-resident QKV
+# weights and four heads' softmax state exceed the VGPRs, the rest goes to AGPRs).
+ATTENTION_TAIL_ROUTE_WIDTHS = frozenset({32, 64})
+ATTENTION_TAIL_MAX_SEQ = 256
 # From this width up the out-projection and FFN run as GEMMs + a separate LayerNorm.
 WIDE_GEMM_FROM = 256
 # GEMM-route widths whose out-projection fuses the next LayerNorm (tiles holding whole
@@ -104,6 +117,7 @@ class Route:
     fuse_attention_output_norm: bool = True
     fuse_full_ffn: bool = True
     fuse_layer_tail: bool = False
+    fuse_attention_tail: bool = False  # head dim 32, d_model <= 64 on the layer-tail route: see attention_tail_for
     wide_ln_epilogue: bool = False
     wide_ln_ffn_out: bool = False
     qkv_variant: int = 0
@@ -126,6 +140,7 @@ class Route:
             "attention_output_norm_fusion": self.fuse_attention_output_norm,
             "full_ffn_fusion": self.fuse_full_ffn,
             "layer_tail_fusion": self.fuse_layer_tail,
+            "attention_in_layer_tail": self.fuse_attention_tail,
             "wide_ln_epilogue": self.wide_ln_epilogue,
             "wide_ln_ffn_out": self.wide_ln_ffn_out,
             "variants": {
@@ -177,6 +192,9 @@ def plan(
         enable_attention_output_norm_fusion and enable_full_ffn_fusion and not narrow
         and d in WIDE_LN_EPILOGUE_WIDTHS
     )
+    fuse_attn_tail = (
+        fuse_tail and hd == 32 and (d, f) in ATTENTION_TAIL_SHAPES and d in ATTENTION_TAIL_ROUTE_WIDTHS
+    )
     route = Route(
         True,
         "hip",
@@ -185,7 +203,19 @@ def plan(
         fuse_attention_output_norm=fuse_out,
         fuse_full_ffn=fuse_ffn,
         fuse_layer_tail=fuse_tail,
+        fuse_attention_tail=fuse_attn_tail,
         wide_ln_epilogue=wide_ln,
         wide_ln_ffn_out=wide_ln and d in WIDE_LN_FFN_OUT_WIDTHS,
     )
     return route
+
+
+def attention_tail_for(route: Route, seq_len: int, masked: bool) -> bool:
+    """Whether a forward over ``seq_len`` positions runs attention inside the layer-tail kernel:
+    the route allows it (head dim 32, a supported tail shape, d_model in
+    ATTENTION_TAIL_ROUTE_WIDTHS), no key mask, and the sequence is whole 64-row tiles of at
+    most ATTENTION_TAIL_MAX_SEQ positions."""
+    return (
+        route.fuse_attention_tail and not masked and 0 < seq_len <= ATTENTION_TAIL_MAX_SEQ
+        and seq_len % ATTENTION_TAIL_ROWS == 0
+    )

@@ -1,5 +1,9 @@
 """Cross-operator fusions of the HIP forward (no single reference function corresponds).
 
+``fused_attention_layer_tail`` runs the causal (or full) attention of head dim 32 in the
+same kernel, from the packed QKV projection, for sequences whose length is a multiple of
+its 64-row tiles (no key mask): one launch per layer instead of two.
+
 ``fused_layer_tail`` composes, with the same rounding points, the reference's
 ``mixed_linear_add_layer_norm`` (attention output projection + residual + LN2),
 ``mixed_ffn_add_layer_norm`` (FFN + residual + next LN) and the next layer's
@@ -19,7 +23,7 @@ import torch
 import torch.nn as nn
 
 from .. import _ops
-from ..dispatch import LAYER_TAIL_SHAPES, LAYERNORM_QKV_WIDTHS
+from ..dispatch import ATTENTION_TAIL_ROWS, ATTENTION_TAIL_SHAPES, LAYER_TAIL_SHAPES, LAYERNORM_QKV_WIDTHS
 from .hip_linear import _fp16_linear_ok, _gpu, _norm_ok
 
 
@@ -94,4 +98,63 @@ def fused_layer_tail(
     return _ops.layer_tail(
         ctx, residual, tensors, None if last else next_qkv_proj.weight, None if last else next_qkv_proj.bias,
         float(norm2.eps), float(next_norm.eps), int(variant),
+    )
+
+
+def attention_layer_tail_supported(d_model: int, ffn_dim: int, heads: int, seq_len: int) -> bool:
+    """Shapes of ``mpk_attention_layer_tail`` (``mpk_attention_layer_tail_supported`` and
+    ``_rows``; the tables are checked against the library by the tests): head dim 32, a
+    layer-tail shape whose LDS also holds the attention tiles, whole 64-row tiles."""
+    d, f, h, s = int(d_model), int(ffn_dim), int(heads), int(seq_len)
+    return (d, f) in ATTENTION_TAIL_SHAPES and h > 0 and d == 32 * h and s > 0 and s % ATTENTION_TAIL_ROWS == 0
+
+
+def fused_attention_layer_tail(
+    qkv: torch.Tensor,
+    residual: torch.Tensor,
+    heads: int,
+    scale: float,
+    causal: bool,
+    out_proj: nn.Linear,
+    norm2: nn.LayerNorm,
+    ffn_in: nn.Linear,
+    ffn_out: nn.Linear,
+    next_norm: nn.LayerNorm,
+    next_qkv_proj: Optional[nn.Linear] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Attention over this layer's packed ``qkv [B, S, 3D]`` (FP16) and everything after it up to
+    the next layer's QKV projection, in one kernel.
+
+    Same arithmetic as ``attention`` (16x16 kernel, 64-key tiles) followed by
+    ``fused_layer_tail``.  Returns ``(residual_out, next qkv)``, or ``(residual_out,
+    next_norm(residual_out))`` in FP32 when ``next_qkv_proj`` is None (last layer).
+    """
+    ok = _gpu(qkv) and qkv.dtype == torch.float16 and qkv.dim() == 3 and qkv.is_contiguous()
+    d = residual.shape[-1] if residual.dim() else 0
+    f = ffn_in.out_features
+    last = next_qkv_proj is None
+    if not (
+        ok
+        and _gpu(residual)
+        and residual.dtype == torch.float32
+        and residual.dim() == 3
+        and residual.is_contiguous()
+        and qkv.shape == (*residual.shape[:-1], 3 * d)
+        and out_proj.in_features == out_proj.out_features == d
+        and ffn_in.in_features == d
+        and ffn_out.in_features == f
+        and ffn_out.out_features == d
+        and all(_fp16_linear_ok(m) for m in (out_proj, ffn_in, ffn_out))
+        and _norm_ok(norm2, d)
+        and _norm_ok(next_norm, d)
+        and (last or (_fp16_linear_ok(next_qkv_proj) and next_qkv_proj.in_features == d
+                      and next_qkv_proj.out_features == 3 * d))
+        and attention_layer_tail_supported(d, f, heads, residual.shape[1])
+    ):
+        raise ValueError("unsupported fused attention layer-tail inputs")
+    tensors = [out_proj.weight, out_proj.bias, norm2.weight, norm2.bias, ffn_in.weight, ffn_in.bias,
+               ffn_out.weight, ffn_out.bias, next_norm.weight, next_norm.bias]
+    return _ops.attention_layer_tail(
+        qkv, residual, tensors, None if last else next_qkv_proj.weight, None if last else next_qkv_proj.bias,
+        int(heads), float(scale), bool(causal), float(norm2.eps), float(next_norm.eps),
     )

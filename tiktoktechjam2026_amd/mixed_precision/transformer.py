@@ -14,7 +14,10 @@ Routes (chosen by ``dispatch.plan`` from the shape):
 
 * layer-tail route (d_model <= 128 with the tail's weights in LDS): one
   LayerNorm+QKV launch, then per layer the flash attention and one fused
-  out-proj + LN2 + FFN + LN1' + next-QKV kernel (mpk_layer_tail);
+  out-proj + LN2 + FFN + LN1' + next-QKV kernel (mpk_layer_tail); at head dim 32 and
+  d_model 32 or 64, without a key mask and for sequences of whole 64-row tiles up to 256
+  positions, the attention runs inside that kernel (mpk_attention_layer_tail: one launch
+  per layer);
 * row-fused route (other d_model <= 128): per layer the QKV projection
   (mpk_linear), attention (mpk_causal_attention), out-projection + residual +
   LayerNorm (mpk_linear_residual_layernorm) and FFN + residual + next
@@ -43,7 +46,7 @@ import torch.nn as nn
 
 from .. import dispatch
 from ..custom_kernel.hip_attention import attention
-from .hip_fused import fused_layer_tail, layer_norm_qkv
+from .hip_fused import fused_attention_layer_tail, fused_layer_tail, layer_norm_qkv
 from .hip_linear import (
     layer_norm,
     mixed_ffn_add_layer_norm,
@@ -285,6 +288,22 @@ def _forward_layer_tail_impl(model: "MixedPrecisionTransformer", x, key_valid, c
     route = model.route
     layers = model.layers
     qkv = layer_norm_qkv(x, layers[0].norm1, layers[0].attention.qkv_proj, variant=route.head_variant)
+    if dispatch.attention_tail_for(route, x.shape[1], key_valid is not None):
+        # 1 + L launches: each layer's attention runs inside its layer-tail kernel
+        result = None
+        for index, layer in enumerate(layers):
+            att = layer.attention
+            last = index + 1 == len(layers)
+            nxt = None if last else layers[index + 1]
+            x, out = fused_attention_layer_tail(
+                qkv, x, att.num_heads, att.scale, causal, att.out_proj, layer.norm2, layer.ffn_in, layer.ffn_out,
+                model.final_norm if last else nxt.norm1, None if last else nxt.attention.qkv_proj,
+            )
+            if last:
+                result = out
+            else:
+                qkv = out
+        return result
     result = None
     for index, layer in enumerate(layers):
         att = layer.attention
