@@ -72,6 +72,28 @@ def test_percentile_matches_linear_interpolation():
         harness.percentile([], 0.5)
     timing = harness.TimingResult([4.0, 1.0, 2.0])
     assert timing.median_ms == 2.0 and timing.min_ms == 1.0 and timing.mean_ms == pytest.approx(7 / 3)
+    assert harness.TimingResult([4.0, 1.0, 2.0, 8.0]).median_ms == 3.0  # even count: midpoint
+
+
+def test_percentile_agrees_with_numpy_linear_method():
+    """numpy's default ("linear", rank q (n - 1)) percentile is the same rule; ends are min / max."""
+    import numpy as np
+
+    rng = np.random.default_rng(7)
+    for n in (1, 2, 3, 10, 101):
+        values = rng.exponential(size=n).tolist()
+        for q in (0.0, 0.1, 0.5, 0.9, 0.99, 1.0):
+            assert harness.percentile(values, q) == pytest.approx(float(np.percentile(values, 100 * q)), rel=1e-12)
+        assert harness.percentile(values, 0.0) == min(values) and harness.percentile(values, 1.0) == max(values)
+
+
+def test_resolve_device():
+    assert harness.resolve_device("cpu") == torch.device("cpu")
+    expected = "cuda" if torch.cuda.is_available() else "cpu"
+    assert harness.resolve_device("auto").type == expected
+    if not torch.cuda.is_available():
+        with pytest.raises(RuntimeError):
+            harness.resolve_device("cuda")
 
 
 def test_generate_random_case_mask_and_seed():

@@ -27,7 +27,6 @@ from __future__ import annotations
 
 import argparse
 import math
-import statistics
 import time
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Tuple
@@ -81,11 +80,13 @@ def seeded_reference_state_dict(config, seed: Optional[int]) -> Dict[str, torch.
 
 
 def resolve_device(device_arg: str) -> torch.device:
-    if device_arg == "auto":
-        return torch.device("cuda" if torch.cuda.is_available() else "cpu")
-    device = torch.device(device_arg)
-    if device.type == "cuda" and not torch.cuda.is_available():
-        raise RuntimeError("CUDA was requested, but torch.cuda.is_available() is False")
+    """``--device`` (``torch_transformer_benchmark.py:428-434``): ``auto`` is the GPU when torch
+    sees one and the CPU otherwise; naming a GPU device that torch cannot see is an error."""
+    gpu_visible = torch.cuda.is_available()
+    name = ("cuda" if gpu_visible else "cpu") if device_arg == "auto" else device_arg
+    device = torch.device(name)
+    if device.type == "cuda" and not gpu_visible:
+        raise RuntimeError(f"--device {device_arg}: torch sees no GPU (torch.cuda.is_available() is False)")
     return device
 
 
@@ -138,6 +139,11 @@ def generate_microbatched_case(
 
 @dataclass
 class AccuracyResult:
+    """One trial of the accuracy check; the field names are those the report prints
+    (``torch_transformer_benchmark.py:489-500``).  ``worst_index`` is the element of the largest
+    absolute error (NaN counts as largest), ``failed_feature_dims`` the last-axis indices
+    holding any failed element."""
+
     passed: bool
     total_elements: int
     failed_elements: int
@@ -260,35 +266,38 @@ def run_accuracy_tests(
 
 
 def percentile(values: List[float], q: float) -> float:
-    """Linear-interpolated percentile (``torch_transformer_benchmark.py:641-653``)."""
-    if not values:
+    """The q-quantile at rank q (n - 1) of the sorted samples, interpolated linearly between
+    the two order statistics around it (numpy's default method) - how the reference's report
+    computes its p90 (``torch_transformer_benchmark.py:641-653``)."""
+    if len(values) == 0:
         raise ValueError("values must not be empty")
     ordered = sorted(values)
-    if len(ordered) == 1:
-        return ordered[0]
-    position = (len(ordered) - 1) * q
-    lower, upper = math.floor(position), math.ceil(position)
-    if lower == upper:
-        return ordered[lower]
-    weight = position - lower
-    return ordered[lower] * (1.0 - weight) + ordered[upper] * weight
+    rank = q * (len(ordered) - 1)
+    below = math.floor(rank)
+    frac = rank - below
+    if frac == 0:
+        return ordered[below]
+    return ordered[below] + frac * (ordered[below + 1] - ordered[below])
 
 
 @dataclass
 class TimingResult:
+    """Per-call latencies (ms) of one timed model and the four figures the report prints from
+    them: mean, median, p90 and minimum (``torch_transformer_benchmark.py:656-674``)."""
+
     samples_ms: List[float]
 
     @property
     def mean_ms(self) -> float:
-        return statistics.fmean(self.samples_ms)
+        return math.fsum(self.samples_ms) / len(self.samples_ms)
 
     @property
     def median_ms(self) -> float:
-        return statistics.median(self.samples_ms)
+        return percentile(self.samples_ms, 0.5)
 
     @property
     def p90_ms(self) -> float:
-        return percentile(self.samples_ms, 0.90)
+        return percentile(self.samples_ms, 0.9)
 
     @property
     def min_ms(self) -> float:
@@ -533,20 +542,23 @@ def parse_args(argv: Optional[List[str]] = None) -> argparse.Namespace:
     return build_parser("Compare a baseline and optimized PyTorch Transformer").parse_args(argv)
 
 
+# Argument checks of ``torch_transformer_benchmark.py:908-922``, in its order: (the condition
+# that rejects the arguments, the message the reference raises for it).
+_ARG_REJECTIONS = (
+    (lambda a: not 0.0 <= a.padding_ratio < 1.0, "padding_ratio must be in [0, 1)"),
+    (lambda a: a.input_scale <= 0, "input_scale must be positive"),
+    (lambda a: a.microbatch_size is not None and a.microbatch_size < 0, "microbatch_size must be non-negative"),
+    (lambda a: a.accuracy_trials <= 0, "accuracy_trials must be positive"),
+    (lambda a: a.rtol < 0 or a.atol < 0, "rtol and atol must be non-negative"),
+    (lambda a: a.warmup < 0, "warmup must be non-negative"),
+    (lambda a: a.repeats <= 0 or a.benchmark_rounds <= 0, "repeats and benchmark_rounds must be positive"),
+)
+
+
 def validate_args(args: argparse.Namespace, device: torch.device, dtype: torch.dtype) -> None:
-    if not 0.0 <= args.padding_ratio < 1.0:
-        raise ValueError("padding_ratio must be in [0, 1)")
-    if args.input_scale <= 0:
-        raise ValueError("input_scale must be positive")
-    if args.microbatch_size is not None and args.microbatch_size < 0:
-        raise ValueError("microbatch_size must be non-negative")
-    if args.accuracy_trials <= 0:
-        raise ValueError("accuracy_trials must be positive")
-    if args.rtol < 0 or args.atol < 0:
-        raise ValueError("rtol and atol must be non-negative")
-    if args.warmup < 0:
-        raise ValueError("warmup must be non-negative")
-    if args.repeats <= 0 or args.benchmark_rounds <= 0:
-        raise ValueError("repeats and benchmark_rounds must be positive")
+    """Raise ``ValueError`` with the first rejection that applies; warn about FP16 on the CPU."""
+    for rejects, message in _ARG_REJECTIONS:
+        if rejects(args):
+            raise ValueError(message)
     if device.type == "cpu" and dtype == torch.float16:
         print("[warning] float16 CPU kernels may be unsupported or slow")
