@@ -171,7 +171,7 @@ int mpk_layer_tail(const void* ctx, const float* x, const void* w_o, const void*
 int mpk_layer_tail_supported(int32_t d, int32_t f);
 
 /*
- * Attention + layer tail in one kernel, for head dim 32 (d == 32 * heads): the causal
+ * Attention + layer tail in one kernel, for head dim 32 (or 16 at d 32 and 64): the causal
  * (or, with causal == 0, full) attention of every row over this layer's packed QKV, then
  * everything mpk_layer_tail does, the context never leaving the registers:
  *   ctx   = attention(qkv_in; heads, scale, causal)   (as mpk_causal_attention, variant 1:
@@ -184,8 +184,9 @@ int mpk_layer_tail_supported(int32_t d, int32_t f);
  * mpk_attention_layer_tail_supported (the layer-tail shapes whose LDS also holds the
  * attention tiles).  One launch per layer instead of mpk_causal_attention + mpk_layer_tail:
  * each 64-row workgroup computes its rows' attention itself, so it pays off for short
- * sequences of narrow models (the module route uses it at d 32 and 64 up to 256 positions,
- * measured 10-20 % faster per forward; d 128 is built but measured slower than two launches).
+ * sequences of narrow models (the module route uses it at d 32 and 64 up to 128-512
+ * positions by shape, measured 3-20 % faster per forward; d 128 is built but measured slower
+ * than two launches).
  * Replaces, fused: fp16_causal_attention (custom_kernel/triton_attention.py:341-390) with
  * the calls mpk_layer_tail replaces; no single reference function corresponds to it.
  */

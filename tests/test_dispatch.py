@@ -78,13 +78,15 @@ def test_python_tables_match_library(built_library):
         assert bool(lib.mpk_layernorm_qkv_supported(d)) == (d in dispatch.LAYERNORM_QKV_WIDTHS)
         for f in (32, 64, 96, 128, 256, 512, 1024, 2048):
             assert bool(lib.mpk_layer_tail_supported(d, f)) == ((d, f) in dispatch.LAYER_TAIL_SHAPES)
-    # attention inside the layer tail: head dim 32 on the tail shapes, whole 64-row tiles
+    # attention inside the layer tail: head dim 32 on the tail shapes, 16 at d_model 32 / 64
     assert lib.mpk_attention_layer_tail_rows() == dispatch.ATTENTION_TAIL_ROWS
     for d in (16, 32, 64, 96, 128, 256):
         for f in (32, 64, 96, 128, 256, 512):
-            for heads in (1, 2, 4, 8):
-                expected = (d, f) in dispatch.ATTENTION_TAIL_SHAPES and d == 32 * heads
+            for heads in (1, 2, 3, 4, 8):
+                expected = dispatch.attention_tail_supported(d, f, heads)
                 assert bool(lib.mpk_attention_layer_tail_supported(d, f, heads)) == expected, (d, f, heads)
+    assert dispatch.attention_tail_supported(32, 64, 2) and dispatch.attention_tail_supported(128, 128, 4)
+    assert not dispatch.attention_tail_supported(128, 128, 8) and not dispatch.attention_tail_supported(64, 64, 1)
     # the wide fused FFN (variant 4, the role-split kernel) is the library's choice exactly
     # where the route fuses it
     for d in (128, 256, 512):
@@ -134,10 +136,10 @@ def test_copy_weights_packs_qkv():
 
 
 def test_attention_in_layer_tail_route():
-    """Head dim 32 with d_model 32 or 64 on the layer-tail route runs attention inside the tail
-    for unmasked sequences of whole 64-row tiles up to 256 positions; d_model 128 (measured
-    slower fused), other head dims, masked forwards, ragged or long sequences keep the
-    separate attention kernel."""
+    """The layer-tail route runs attention inside the tail for unmasked sequences of whole
+    64-row tiles up to the measured length of its (d_model, head dim) (d_model 32 and 64, head
+    dim 32 or 16); d_model 128 (measured slower fused), other head dims, masked forwards,
+    ragged or longer sequences keep the separate attention kernel."""
     from tiktoktechjam2026_amd.config import TransformerConfig
 
     d64 = dispatch.plan(TransformerConfig(2, 128, 64, 2, 128, 2, True))  # hd 32
@@ -148,7 +150,13 @@ def test_attention_in_layer_tail_route():
     assert not dispatch.attention_tail_for(d64, 100, masked=False)   # ragged tiles
     assert not dispatch.attention_tail_for(d64, 512, masked=False)   # long: the attention kernel
     assert dispatch.plan(TransformerConfig(2, 64, 32, 1, 64, 2, True)).fuse_attention_tail  # D32 H1
+    cfg3 = dispatch.plan(BENCHMARK_CONFIGS["cfg3"])  # D32 H2: hd 16
+    assert cfg3.fuse_attention_tail and dispatch.attention_tail_for(cfg3, 256, masked=False)
+    assert dispatch.attention_tail_for(cfg3, 512, masked=False) and not dispatch.attention_tail_for(cfg3, 1024, False)
+    d64h16 = dispatch.plan(TransformerConfig(2, 128, 64, 4, 128, 2, True))  # hd 16
+    assert dispatch.attention_tail_for(d64h16, 128, False) and not dispatch.attention_tail_for(d64h16, 256, False)
     cfg1 = dispatch.plan(BENCHMARK_CONFIGS["cfg1"])  # D128 H4: hd 32, but d_model 128
     assert cfg1.fuse_layer_tail and not cfg1.fuse_attention_tail
-    assert not dispatch.plan(BENCHMARK_CONFIGS["cfg3"]).fuse_attention_tail  # D32 H2: hd 16
     assert not dispatch.plan(TransformerConfig(2, 64, 64, 1, 64, 2, True)).fuse_attention_tail  # hd 64
+    for (d, hd) in dispatch.ATTENTION_TAIL_ROUTE_MAX_SEQ:
+        assert any(dispatch.attention_tail_supported(d, f, d // hd) for (dd, f) in dispatch.LAYER_TAIL_SHAPES if dd == d)

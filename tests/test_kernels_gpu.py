@@ -687,21 +687,22 @@ def _check_layer_tail(hip_device, d, f, m, last, variant):
 # --------------------------------------------------------------------------- attention inside the layer tail
 
 
-@pytest.mark.parametrize("d,f", [(128, 128), (64, 256), (64, 64), (32, 32), (32, 128)])
+@pytest.mark.parametrize("d,f,heads", [(128, 128, 4), (64, 256, 2), (64, 64, 2), (32, 32, 1), (32, 128, 1),
+                                         (32, 64, 2), (64, 128, 4), (32, 32, 2)])
 @pytest.mark.parametrize("b,s", [(1, 64), (3, 128), (2, 256)])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("last", [False, True])
-def test_attention_layer_tail_matches_two_kernels(hip_device, d, f, b, s, causal, last):
-    """mpk_attention_layer_tail equals mpk_causal_attention (variant 1: the 16x16 kernel,
-    64-key tiles) followed by mpk_layer_tail (variant 3: 4 waves x 16 rows), bit for bit:
+def test_attention_layer_tail_matches_two_kernels(hip_device, d, f, heads, b, s, causal, last):
+    """mpk_attention_layer_tail (head dim 32 or 16) equals mpk_causal_attention (variant 1: the
+    16x16 kernel, 64-key tiles) followed by mpk_layer_tail (variant 3: 4 waves x 16 rows), bit for bit:
     the attention stage runs the same arithmetic over the same tiles, and the tail is the
     same kernel.  The two-kernel result is itself checked against float64 by the tests
     above."""
     from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention
     from tiktoktechjam2026_amd.mixed_precision.hip_fused import fused_attention_layer_tail, fused_layer_tail
 
-    heads = d // 32
-    print(f"\n[attention tail] d={d} f={f} b={b} s={s} causal={causal} last={last}", flush=True)
+    hd = d // heads
+    print(f"\n[attention tail] d={d} f={f} heads={heads} b={b} s={s} causal={causal} last={last}", flush=True)
     qkv = (_randn((b, s, 3 * d), 71, 1.5)).to(hip_device, torch.float16)
     x = _randn((b, s, d), 72, 2.0).to(hip_device)
     out_proj = _linear(d, d, hip_device, 73)
@@ -710,10 +711,10 @@ def test_attention_layer_tail_matches_two_kernels(hip_device, d, f, b, s, causal
     norm2 = _norm(d, hip_device, 76)
     next_norm = _norm(d, hip_device, 77)
     qkv_proj = None if last else _linear(d, 3 * d, hip_device, 78)
-    scale = 32 ** -0.5
+    scale = hd ** -0.5
     x_f, out_f = fused_attention_layer_tail(qkv, x, heads, scale, causal, out_proj, norm2, ffn_in, ffn_out,
                                             next_norm, qkv_proj)
-    q, k, v = qkv.view(b, s, 3, heads, 32).permute(2, 0, 3, 1, 4).unbind(0)
+    q, k, v = qkv.view(b, s, 3, heads, hd).permute(2, 0, 3, 1, 4).unbind(0)
     ctx = attention(q, k, v, scale, causal=causal, variant=1).reshape(b, s, d)
     x_u, out_u = fused_layer_tail(ctx, x, out_proj, norm2, ffn_in, ffn_out, next_norm, qkv_proj, variant=3)
     assert torch.equal(x_f, x_u), (x_f - x_u).abs().max().item()
@@ -729,7 +730,7 @@ def test_attention_layer_tail_rejects(hip_device):
     d, f = 128, 128
     mods = [_linear(d, d, hip_device, 1), _norm(d, hip_device, 2), _linear(d, f, hip_device, 3),
             _linear(f, d, hip_device, 4), _norm(d, hip_device, 5), _linear(d, 3 * d, hip_device, 6)]
-    for s, heads in ((96, 4), (128, 2)):
+    for s, heads in ((96, 4), (128, 2), (128, 8)):  # ragged; head dim 64; head dim 16 at d_model 128
         qkv = torch.zeros(1, s, 3 * d, device=hip_device, dtype=torch.float16)
         x = torch.zeros(1, s, d, device=hip_device)
         with pytest.raises(ValueError):

@@ -246,9 +246,9 @@ def test_layer_tail_route_matches_per_op_route(hip_device, name):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("d,heads,f", [(64, 2, 128), (32, 1, 64), (128, 4, 128)])
+@pytest.mark.parametrize("d,heads,f", [(64, 2, 128), (32, 1, 64), (128, 4, 128), (32, 2, 64), (64, 4, 128)])
 def test_attention_in_layer_tail_route_is_bit_identical(hip_device, causal, d, heads, f):
-    """Head dim 32 at 128 positions with attention inside each layer's layer-tail kernel
+    """Head dim 32 (or 16) at 128 positions with attention inside each layer's layer-tail kernel
     (1 + L launches; the route's choice at d_model 32 and 64, forced at 128) gives the output
     of the two-kernel route (attention + layer tail, 1 + 2L launches) bit for bit."""
     from tiktoktechjam2026_amd import dispatch
@@ -256,7 +256,7 @@ def test_attention_in_layer_tail_route_is_bit_identical(hip_device, causal, d, h
     config = TransformerConfig(16, 128, d, heads, f, 4, causal)
     _, model = _build(config, hip_device)
     assert dispatch.attention_tail_for(model.route, 128, masked=False) == (d <= 64)
-    model.route = dataclasses.replace(model.route, fuse_attention_tail=True)
+    model.route = dataclasses.replace(model.route, fuse_attention_tail=True, attention_tail_max_seq=128)
     x = torch.randn(16, 128, d, generator=torch.Generator().manual_seed(9)).to(hip_device)
     with torch.inference_mode():
         fused = model(x)

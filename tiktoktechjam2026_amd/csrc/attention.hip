@@ -246,6 +246,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = (float)(_Float16)src[j] * a.c;
       }
+      pin_f32x4(v);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         qh16[t][j] = (_Float16)v[j];
@@ -255,11 +256,14 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 #pragma unroll
       for (int kq = 0; kq < QK_STEPS; ++kq) {
         const h8 raw = q < S ? load8_as_half(Q + (int64_t)q * a.qs[2] + kq * 32 + 8 * g) : zero_h8();
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (float)raw[j] * a.c;
+        pin_f32x8(v);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float v = (float)raw[j] * a.c;
-          qh[t][kq][j] = (_Float16)v;
-          ql[t][kq][j] = (_Float16)(v - (float)qh[t][kq][j]);
+          qh[t][kq][j] = (_Float16)v[j];
+          ql[t][kq][j] = (_Float16)(v[j] - (float)qh[t][kq][j]);
         }
       }
     }
@@ -570,8 +574,12 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
     if constexpr (HP == 16) {
       // lane group g holds d = 4g .. 4g+3
       if (4 * g < HD) {
+        float o[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[4 * g + i] = (OT)(oacc[t][0][0][i] * inv);
+        for (int i = 0; i < 4; ++i) o[i] = oacc[t][0][0][i] * inv;
+        pin_f32x4(o);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[4 * g + i] = (OT)o[i];
       }
     } else {
 #pragma unroll
@@ -582,6 +590,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
           v[i] = oacc[t][dt][0][i] * inv;
           v[4 + i] = oacc[t][dt][1][i] * inv;
         }
+        pin_f32x8(v);
         store8(dst + 32 * dt + 8 * g, v);
       }
     }
@@ -1101,6 +1110,7 @@ void attention32_kernel(AttnArgs a) {
         float v[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = oacc[dt][8 * s2 + j] * inv;
+        pin_f32x8(v);
         store8(dst + 32 * dt + 16 * s2 + 8 * hf, v);
       }
   }

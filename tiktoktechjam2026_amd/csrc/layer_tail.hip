@@ -218,37 +218,48 @@ __device__ __forceinline__ void load_tile(TileIn<D, TM, STAGE1>& in, const TailA
   }
 }
 
-// ---- attention stage (head dim 32) of the fused attention + layer-tail kernel ----
+// ---- attention stage (head dim HD = 32 or 16) of the fused attention + layer-tail kernel ----
 // The context of a wave's 16 TM rows, computed in the kernel instead of read from HBM: per
-// head, the arithmetic of attention_kernel<32, TM, 64, W, FP16 in/out, no key mask>
-// (attention.hip) - q c split into FP16 hi + lo, S^T = K (q c)^T - m on 16x16x32 MFMAs
-// (the accumulator starts at -m), a running max raised lazily (by more than kRescaleLog2
-// only), p = exp2(.) rounded to FP16, l and O^T = V^T P^T by MFMAs, o = O / l - over the
-// same 64-key tiles, so the context is bit-identical to that kernel's.  Lane (r, g) ends
-// with dims 8g .. 8g + 7 of head h of row 16 t + r: exactly the B-operand fragment
-// ctx[t][h] that the out-projection's k-step h reads.  All rows of the workgroup lie in
-// one sequence (the launcher checks seq % rows == 0).
+// head, the arithmetic of attention_kernel<HD, TM, 64, W, FP16 in/out, no key mask>
+// (attention.hip) - q c split into FP16 hi + lo, S^T = K (q c)^T - m on 16x16x32 (hd 32)
+// or 16x16x16 (hd 16) MFMAs (the accumulator starts at -m), a running max raised lazily
+// (by more than kRescaleLog2 only), p = exp2(.) rounded to FP16, l and O^T = V^T P^T by
+// MFMAs, o = fp16(O / l) - over the same 64-key tiles, so the context is bit-identical to
+// that kernel's output.  It ends as the out-projection's B operand: lane (r, g) holds
+// features 32 ks + 8g .. +7 of row 16 t + r in ctx[t][ks].  At hd 32 that is where the
+// PV product leaves head ks; at hd 16 (lane group g holds dims 4g .. 4g+3 of a head) the
+// wave passes its rows through a private LDS area.  All rows of the workgroup lie in one
+// sequence (the launcher checks seq % rows == 0).
 // A step is one 64-key tile of every head: the workgroup's rows are few (64), so a step per
 // (head, tile) would leave each step bound by a memory latency; a step per tile exposes one
-// latency per tile at most.  The tiles go through NB LDS buffers (2 where they fit beside
-// the weights, else 1 with the next tile held in registers across the step).
+// latency per tile at most, and the heads' softmax chains run interleaved in one wave.  The
+// tiles go through NB LDS buffers (2 where they fit beside the weights, else 1 with the
+// next tile held in registers across the step).
 constexpr int kAttnKT = 64;                     // keys per tile
-constexpr int kAttnLDK = 40;                    // K tile row stride (halves; 16-byte padded)
 constexpr int kAttnLDV = kAttnKT + 8;           // V^T tile row stride (halves)
-constexpr int kAttnKBuf = kAttnKT * kAttnLDK;   // halves per K tile of one head
-constexpr int kAttnVBuf = 32 * kAttnLDV;        // halves per V^T tile of one head
+template <int HD>
+struct AttnTile {
+  static constexpr int LDK = HD + 8;            // K tile row stride (halves; 16-byte padded)
+  static constexpr int KBUF = kAttnKT * LDK;    // halves per K tile of one head
+  static constexpr int VBUF = HD * kAttnLDV;    // halves per V^T tile of one head
+};
 // bytes of one buffer: K and V^T tiles of every head, then the key bias [KT] (floats)
-template <int D>
-constexpr int attn_buf_bytes() { return (D / 32) * (kAttnKBuf + kAttnVBuf) * 2 + kAttnKT * 4; }
+template <int D, int HD>
+constexpr int attn_buf_bytes() {
+  return (D / HD) * (AttnTile<HD>::KBUF + AttnTile<HD>::VBUF) * 2 + kAttnKT * 4;
+}
+// hd 16: each wave's rows of the context (FP16), after the buffers
+template <int D, int HD, int TM, int W>
+constexpr int attn_xchg_bytes() { return HD == 16 ? W * 16 * TM * D * 2 : 0; }
 
 // Registers of the attention stage's global reads: one K / V tile of every head with its
 // key bias, and the wave's raw queries.  The queries are read (and split) before the first
 // tile is requested; issuing the first tile's reads earlier, ahead of the weight prologue,
 // measured slower at d_model 128 (registers held across the prologue push the
 // register-resident QKV weights into AGPRs).
-template <int D, int TM, int W>
+template <int D, int HD, int TM, int W>
 struct AttnRegs {
-  static constexpr int H = D / 32;
+  static constexpr int H = D / HD;
   static constexpr int NT = 64 * W;
   static constexpr int KT = kAttnKT;
   static constexpr int CPR = D / 8;                    // 16-byte chunks of a key's K (or V) row
@@ -257,7 +268,9 @@ struct AttnRegs {
   static constexpr int VITEMS = (KT / 2) * CPR;        // V tile: a key pair x one chunk per item
   static constexpr int V_PER_THREAD = (VITEMS + NT - 1) / NT;
   static constexpr int U = H * TM;                     // row tiles u = h TM + t
-  h8 kreg[PER_THREAD], vreg[V_PER_THREAD][2], qraw[U];
+  h8 kreg[PER_THREAD], vreg[V_PER_THREAD][2];
+  h8 qraw[HD == 32 ? U : 1];
+  h4 qraw16[HD == 16 ? U : 1];
   float breg;
 
   // K and V rows kb .. kb + KT - 1 of every head of the sequence at seq (S positions)
@@ -286,38 +299,49 @@ struct AttnRegs {
     }
     breg = kb + (int)threadIdx.x < S ? 0.f : -INFINITY;
   }
-  // lane (r, g): query row qw0 + 16 t + r, dims 8g .. 8g + 7 of head h, for u = h TM + t
+  // lane (r, g): query row qw0 + 16 t + r of head h, for u = h TM + t: dims 8g .. 8g + 7
+  // (hd 32) or 4g .. 4g + 3 (hd 16)
   __device__ __forceinline__ void load_q(const _Float16* seq, int S, int qw0, int r, int g) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int q = qw0 + 16 * (u % TM) + r;
-      qraw[u] = q < S ? *reinterpret_cast<const h8*>(seq + (int64_t)q * (3 * D) + 32 * (u / TM) + 8 * g) : zero_h8();
+      const _Float16* src = seq + (int64_t)q * (3 * D) + HD * (u / TM);
+      if constexpr (HD == 32) {
+        qraw[u] = q < S ? *reinterpret_cast<const h8*>(src + 8 * g) : zero_h8();
+      } else {
+        h4 z;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) z[j] = (_Float16)0.0f;
+        qraw16[u] = q < S ? *reinterpret_cast<const h4*>(src + 4 * g) : z;
+      }
     }
   }
 };
 
-template <int D, int TM, int W, int NB>
+template <int D, int HD, int TM, int W, int NB>
 __device__ __forceinline__ void tail_attention(const TailArgs& a, unsigned char* att_lds, int64_t wg0,
                                                h8 (&ctx)[TM][D / 32]) {
   static_assert(NB == 1 || NB == 2, "one or two tile buffers");
-  constexpr int H = D / 32;
+  static_assert(HD == 16 || HD == 32, "head dim");
+  constexpr int H = D / HD;
   constexpr int NT = 64 * W;
   constexpr int ROWS = 16 * TM * W;
   constexpr int KT = kAttnKT;
   constexpr int NP = KT / 32;                          // key pairs per tile
-  using R = AttnRegs<D, TM, W>;
+  using R = AttnRegs<D, HD, TM, W>;
+  using AT = AttnTile<HD>;
   R st;
   constexpr int CPR = R::CPR, CHUNKS = R::CHUNKS, PER_THREAD = R::PER_THREAD;
   constexpr int VITEMS = R::VITEMS, V_PER_THREAD = R::V_PER_THREAD;
-  constexpr int BUF = attn_buf_bytes<D>();
+  constexpr int BUF = attn_buf_bytes<D, HD>();
   auto ks_of = [&](int buf, int h) {
-    return reinterpret_cast<_Float16*>(att_lds + buf * BUF) + h * kAttnKBuf;
+    return reinterpret_cast<_Float16*>(att_lds + buf * BUF) + h * AT::KBUF;
   };
   auto vt_of = [&](int buf, int h) {
-    return reinterpret_cast<_Float16*>(att_lds + buf * BUF) + H * kAttnKBuf + h * kAttnVBuf;
+    return reinterpret_cast<_Float16*>(att_lds + buf * BUF) + H * AT::KBUF + h * AT::VBUF;
   };
   auto kbias_of = [&](int buf) {
-    return reinterpret_cast<float*>(reinterpret_cast<_Float16*>(att_lds + buf * BUF) + H * (kAttnKBuf + kAttnVBuf));
+    return reinterpret_cast<float*>(reinterpret_cast<_Float16*>(att_lds + buf * BUF) + H * (AT::KBUF + AT::VBUF));
   };
 
   const int S = a.seq;
@@ -342,7 +366,7 @@ __device__ __forceinline__ void tail_attention(const TailArgs& a, unsigned char*
       const int cc = threadIdx.x + i * NT;
       if (cc < CHUNKS) {
         const int key = cc / CPR, col = (cc % CPR) * 8;
-        *reinterpret_cast<h8*>(&ks_of(buf, col / 32)[key * kAttnLDK + col % 32]) = st.kreg[i];
+        *reinterpret_cast<h8*>(&ks_of(buf, col / HD)[key * AT::LDK + col % HD]) = st.kreg[i];
       }
     }
 #pragma unroll
@@ -350,14 +374,14 @@ __device__ __forceinline__ void tail_attention(const TailArgs& a, unsigned char*
       const int cc = threadIdx.x + i * NT;
       if (cc < VITEMS) {
         const int kp = cc % (KT / 2), col = (cc / (KT / 2)) * 8;
-        _Float16* vt = vt_of(buf, col / 32);
+        _Float16* vt = vt_of(buf, col / HD);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           typedef _Float16 h2 __attribute__((ext_vector_type(2)));
           h2 pair;
           pair[0] = st.vreg[i][0][j];
           pair[1] = st.vreg[i][1][j];
-          *reinterpret_cast<h2*>(&vt[(col % 32 + j) * kAttnLDV + 2 * kp]) = pair;
+          *reinterpret_cast<h2*>(&vt[(col % HD + j) * kAttnLDV + 2 * kp]) = pair;
         }
       }
     }
@@ -367,30 +391,50 @@ __device__ __forceinline__ void tail_attention(const TailArgs& a, unsigned char*
   // Row tiles u = h TM + t (head h, rows 16 t ..): every step below runs over all of them,
   // so a wave has H TM independent chains (it is alone on its SIMD at these sizes).
   constexpr int U = H * TM;
-  // q c in FP32, split into FP16 hi + lo (lane (r, g): query row 16 t + r, dims 8g .. 8g + 7 of head h)
+  constexpr int DT = HD == 32 ? 2 : 1;                 // O^T accumulators per row tile
+  // q c in FP32, split into FP16 hi + lo.  Every FP32 value that is then converted to FP16
+  // (q c here, o / l at the end) is pinned first (pin_f32), as in attention_kernel, so both
+  // round to FP32 and then to FP16.
   st.load_q(seq, S, qw0, r, g);
-  h8 qh[U], ql[U];
+  h8 qh[HD == 32 ? U : 1], ql[HD == 32 ? U : 1];
+  h4 qh16[HD == 16 ? U : 1], ql16[HD == 16 ? U : 1];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
+    if constexpr (HD == 32) {
+      float v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float v = (float)st.qraw[u][j] * c;
-      qh[u][j] = (_Float16)v;
-      ql[u][j] = (_Float16)(v - (float)qh[u][j]);
+      for (int j = 0; j < 8; ++j) v[j] = (float)st.qraw[u][j] * c;
+      pin_f32x8(v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        qh[u][j] = (_Float16)v[j];
+        ql[u][j] = (_Float16)(v[j] - (float)qh[u][j]);
+      }
+    } else {
+      float v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = (float)st.qraw16[u][j] * c;
+      pin_f32x4(v);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        qh16[u][j] = (_Float16)v[j];
+        ql16[u][j] = (_Float16)(v[j] - (float)qh16[u][j]);
+      }
     }
   }
   float mrow[U];
   bool fresh[U];
-  f4 oacc[U][2], lsum_acc[U];
+  f4 oacc[U][DT], lsum_acc[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     mrow[u] = 0.f;
     fresh[u] = true;
     lsum_acc[u] = zero4();
-    oacc[u][0] = oacc[u][1] = zero4();
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) oacc[u][dt] = zero4();
   }
 
-  // one key tile of every head: S^T, online softmax, O^T += V^T P^T (attention_kernel's process, hd 32)
+  // one key tile of every head: S^T, online softmax, O^T += V^T P^T (attention_kernel's process)
   auto process_all = [&](const int kb, const int buf, auto first_tag) {
     constexpr bool MAYBE_FRESH = decltype(first_tag)::value;
     if (a.causal && kb > qw_last) return;  // whole tile is in this wave's future
@@ -410,13 +454,24 @@ __device__ __forceinline__ void tail_attention(const TailArgs& a, unsigned char*
           const float c0 = (MAYBE_FRESH && fresh[u]) ? 0.f : -mrow[u];
           sc[p][tt][u] = f4{c0, c0, c0, c0};
         }
-        h8 ka[H];
+        if constexpr (HD == 32) {
+          h8 ka[H];
 #pragma unroll
-        for (int h = 0; h < H; ++h) ka[h] = *reinterpret_cast<const h8*>(&ks_of(buf, h)[krow * kAttnLDK + 8 * g]);
+          for (int h = 0; h < H; ++h) ka[h] = *reinterpret_cast<const h8*>(&ks_of(buf, h)[krow * AT::LDK + 8 * g]);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          sc[p][tt][u] = mfma32(ka[u / TM], qh[u], sc[p][tt][u]);
-          sc[p][tt][u] = mfma32(ka[u / TM], ql[u], sc[p][tt][u]);
+          for (int u = 0; u < U; ++u) {
+            sc[p][tt][u] = mfma32(ka[u / TM], qh[u], sc[p][tt][u]);
+            sc[p][tt][u] = mfma32(ka[u / TM], ql[u], sc[p][tt][u]);
+          }
+        } else {
+          h4 ka[H];
+#pragma unroll
+          for (int h = 0; h < H; ++h) ka[h] = *reinterpret_cast<const h4*>(&ks_of(buf, h)[krow * AT::LDK + 4 * g]);
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            sc[p][tt][u] = mfma16(ka[u / TM], qh16[u], sc[p][tt][u]);
+            sc[p][tt][u] = mfma16(ka[u / TM], ql16[u], sc[p][tt][u]);
+          }
         }
       }
     }
@@ -477,8 +532,8 @@ __device__ __forceinline__ void tail_attention(const TailArgs& a, unsigned char*
         if (shift_row && !is_fresh) {
           const float alpha = __builtin_amdgcn_exp2f(-shift);
           lsum_acc[u] *= alpha;
-          oacc[u][0] *= alpha;
-          oacc[u][1] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) oacc[u][dt] *= alpha;
         }
         if (shift_row) {
           mrow[u] = is_fresh ? shift : mrow[u] + shift;
@@ -506,18 +561,28 @@ __device__ __forceinline__ void tail_attention(const TailArgs& a, unsigned char*
           for (int i = 0; i < 4; ++i) pf[u][4 * tt + i] = (_Float16)__builtin_amdgcn_exp2f(sc[p][tt][u][i]);
 #pragma unroll
       for (int u = 0; u < U; ++u) lsum_acc[u] = mfma32(ones_row, pf[u], lsum_acc[u]);
+      if constexpr (HD == 32) {
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int drow = pair_row(r, tt);
+        for (int tt = 0; tt < 2; ++tt) {
+          const int drow = pair_row(r, tt);
+          h8 va[H];
+#pragma unroll
+          for (int h = 0; h < H; ++h) va[h] = *reinterpret_cast<const h8*>(&vt_of(buf, h)[drow * kAttnLDV + 32 * p + 8 * g]);
+#pragma unroll
+          for (int u = 0; u < U; ++u) oacc[u][tt] = mfma32(va[u / TM], pf[u], oacc[u][tt]);
+        }
+      } else {
         h8 va[H];
 #pragma unroll
-        for (int h = 0; h < H; ++h) va[h] = *reinterpret_cast<const h8*>(&vt_of(buf, h)[drow * kAttnLDV + 32 * p + 8 * g]);
+        for (int h = 0; h < H; ++h) va[h] = *reinterpret_cast<const h8*>(&vt_of(buf, h)[r * kAttnLDV + 32 * p + 8 * g]);
 #pragma unroll
-        for (int u = 0; u < U; ++u) oacc[u][tt] = mfma32(va[u / TM], pf[u], oacc[u][tt]);
+        for (int u = 0; u < U; ++u) oacc[u][0] = mfma32(va[u / TM], pf[u], oacc[u][0]);
       }
     }
   };
 
+  // the first tile is requested after the queries; the caller's previous LDS use of this
+  // area (the QKV row ring) must be finished before it is stashed
   st.fetch(seq, S, 0);
   __syncthreads();
   stash(0);
@@ -536,33 +601,63 @@ __device__ __forceinline__ void tail_attention(const TailArgs& a, unsigned char*
     }
     __syncthreads();  // the stashed tile is visible; the last one also frees the area
   }
+  if constexpr (HD == 32) {
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const float lsum = sum_over_groups(lsum_acc[u][0]);
-    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    for (int u = 0; u < U; ++u) {
+      const float lsum = sum_over_groups(lsum_acc[u][0]);
+      const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+      float o[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ctx[u % TM][u / TM][i] = (_Float16)(oacc[u][0][i] * inv);
-      ctx[u % TM][u / TM][4 + i] = (_Float16)(oacc[u][1][i] * inv);
+      for (int i = 0; i < 4; ++i) {
+        o[i] = oacc[u][0][i] * inv;
+        o[4 + i] = oacc[u][1][i] * inv;
+      }
+      pin_f32x8(o);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ctx[u % TM][u / TM][i] = (_Float16)o[i];
     }
+  } else {
+    // lane (r, g) holds dims 4g .. 4g+3 of head h for row 16 t + r: through this wave's LDS rows
+    _Float16* xw = reinterpret_cast<_Float16*>(att_lds + NB * BUF) + wave * (16 * TM * D);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float lsum = sum_over_groups(lsum_acc[u][0]);
+      const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+      float of[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) of[i] = oacc[u][0][i] * inv;
+      pin_f32x4(of);
+      h4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = (_Float16)of[i];
+      *reinterpret_cast<h4*>(&xw[(16 * (u % TM) + r) * D + HD * (u / TM) + 4 * g]) = o;
+    }
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+      for (int ks = 0; ks < D / 32; ++ks)
+        ctx[t][ks] = *reinterpret_cast<const h8*>(&xw[(16 * t + r) * D + 32 * ks + 8 * g]);
   }
 }
 
 // LDS of the fused kernel: two attention buffers where they fit, else one
-template <int D, int F, int TM, bool QKV, int QMODE, int W>
+template <int D, int F, int TM, bool QKV, int QMODE, int W, int AHD>
 constexpr int attn_nbuf() {
   using SH = TailShape<D, F, TM, true, QKV, QMODE, W, true>;
-  return SH::ATT_OFF_BYTES + 2 * attn_buf_bytes<D>() <= kLdsBudget ? 2 : 1;
+  return SH::ATT_OFF_BYTES + 2 * attn_buf_bytes<D, AHD>() + attn_xchg_bytes<D, AHD, TM, W>() <= kLdsBudget ? 2 : 1;
 }
-template <int D, int F, int TM, bool QKV, int QMODE, int W>
+template <int D, int F, int TM, bool QKV, int QMODE, int W, int AHD>
 constexpr int attn_lds_bytes() {
   using SH = TailShape<D, F, TM, true, QKV, QMODE, W, true>;
-  constexpr int att = SH::ATT_OFF_BYTES + attn_nbuf<D, F, TM, QKV, QMODE, W>() * attn_buf_bytes<D>();
+  constexpr int att = SH::ATT_OFF_BYTES + attn_nbuf<D, F, TM, QKV, QMODE, W, AHD>() * attn_buf_bytes<D, AHD>() +
+                      attn_xchg_bytes<D, AHD, TM, W>();
   return att > SH::BYTES ? att : SH::BYTES;
 }
 
-template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE, int W, bool ATTN = false>
+// AHD: 0, or the head dim (16, 32) of the attention stage computed in the kernel.
+template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE, int W, int AHD = 0>
 __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
+  constexpr bool ATTN = AHD != 0;
   static_assert(!ATTN || STAGE1, "the attention stage feeds the out-projection");
   constexpr bool QKV = !LAST;
   constexpr int NT = 64 * W;
@@ -645,7 +740,7 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
     const int64_t wg0 = tile * ROWS;
     const int64_t m0 = wg0 + wave * 16 * TM;
     if constexpr (ATTN) {
-      tail_attention<D, TM, W, attn_nbuf<D, F, TM, QKV, QMODE, W>()>(
+      tail_attention<D, AHD, TM, W, attn_nbuf<D, F, TM, QKV, QMODE, W, AHD>()>(
           a, reinterpret_cast<unsigned char*>(lds) + SH::ATT_OFF_BYTES, wg0, cur.ctx);
     }
     // rows of this wave / workgroup that exist (stores to the others are dropped by the buffer resource)
@@ -915,12 +1010,19 @@ static int tail_cu_count() {
   return cached[dev];
 }
 
-template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE, int W, bool ATTN = false>
+template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE, int W, int AHD>
+constexpr int tail_lds_bytes() {
+  if constexpr (AHD != 0)
+    return attn_lds_bytes<D, F, TM, !LAST, QMODE, W, AHD>();
+  else
+    return TailShape<D, F, TM, STAGE1, !LAST, QMODE, W>::BYTES;
+}
+
+template <int D, int F, int TM, bool STAGE1, bool LAST, int QMODE, int W, int AHD = 0>
 static hipError_t launch_tail(const TailArgs& a, hipStream_t s) {
-  constexpr int lds_bytes = ATTN ? attn_lds_bytes<D, F, TM, !LAST, QMODE, W>()
-                                 : TailShape<D, F, TM, STAGE1, !LAST, QMODE, W>::BYTES;
+  constexpr int lds_bytes = tail_lds_bytes<D, F, TM, STAGE1, LAST, QMODE, W, AHD>();
   static_assert(lds_bytes <= kLdsBudget, "weights exceed LDS");
-  auto kern = layer_tail_kernel<D, F, TM, STAGE1, LAST, QMODE, W, ATTN>;
+  auto kern = layer_tail_kernel<D, F, TM, STAGE1, LAST, QMODE, W, AHD>;
   if (lds_bytes > 64 * 1024) {
     static std::atomic<bool> attribute_set{false};  // once per instantiation
     if (!attribute_set.load(std::memory_order_acquire)) {
@@ -965,22 +1067,32 @@ static int tail_auto_variant(int64_t m) { return (m + 127) / 128 < tail_cu_count
 
 // Fused attention + tail: 4 waves x 16 rows (64-row tiles; a tile's rows lie in one
 // sequence when seq % 64 == 0), where the weights, parameters and the attention area fit.
+// Head dims 32 (any of the tail widths) and 16 (d_model 32 and 64).
 constexpr int kAttnTailRows = 64;
-template <int D, int F>
+template <int D, int F, int AHD>
 constexpr bool attn_tail_fits() {
   constexpr int QM = qkv_mode<D, F, true>();
-  return (QM != kQkvReg || (3 * D) % (16 * 4) == 0) &&
-         attn_lds_bytes<D, F, 1, true, QM, 4>() <= kLdsBudget;
+  return D % AHD == 0 && (AHD == 32 || D <= 64) && (QM != kQkvReg || (3 * D) % (16 * 4) == 0) &&
+         attn_lds_bytes<D, F, 1, true, QM, 4, AHD>() <= kLdsBudget;
 }
-template <int D, int F>
-static hipError_t attn_tail_launch(bool last, const TailArgs& a, hipStream_t s) {
-  if constexpr (attn_tail_fits<D, F>()) {
+template <int D, int F, int AHD>
+static hipError_t attn_tail_launch_hd(bool last, const TailArgs& a, hipStream_t s) {
+  if constexpr (attn_tail_fits<D, F, AHD>()) {
     constexpr int QM = qkv_mode<D, F, true>();
-    return last ? launch_tail<D, F, 1, true, true, QM, 4, true>(a, s) : launch_tail<D, F, 1, true, false, QM, 4, true>(a, s);
+    return last ? launch_tail<D, F, 1, true, true, QM, 4, AHD>(a, s)
+                : launch_tail<D, F, 1, true, false, QM, 4, AHD>(a, s);
   } else {
     (void)last; (void)a; (void)s;
     return (hipError_t)MPK_EUNSUPPORTED;
   }
+}
+template <int D, int F>
+static bool attn_tail_fits_hd(int hd) {
+  return hd == 32 ? attn_tail_fits<D, F, 32>() : hd == 16 ? attn_tail_fits<D, F, 16>() : false;
+}
+template <int D, int F>
+static hipError_t attn_tail_launch(int hd, bool last, const TailArgs& a, hipStream_t s) {
+  return hd == 32 ? attn_tail_launch_hd<D, F, 32>(last, a, s) : attn_tail_launch_hd<D, F, 16>(last, a, s);
 }
 
 }  // namespace mpk
@@ -1033,14 +1145,15 @@ extern "C" int mpk_layer_tail(const void* ctx, const float* x, const void* w_o, 
 }
 
 extern "C" int mpk_attention_layer_tail_supported(int32_t d, int32_t f, int32_t heads) {
-  if (!mpk_layer_tail_supported(d, f) || heads <= 0 || d != 32 * heads) return 0;
-  if (d == 32 && f == 32) return attn_tail_fits<32, 32>();
-  if (d == 32 && f == 64) return attn_tail_fits<32, 64>();
-  if (d == 32 && f == 128) return attn_tail_fits<32, 128>();
-  if (d == 64 && f == 64) return attn_tail_fits<64, 64>();
-  if (d == 64 && f == 128) return attn_tail_fits<64, 128>();
-  if (d == 64 && f == 256) return attn_tail_fits<64, 256>();
-  return attn_tail_fits<128, 128>();
+  if (!mpk_layer_tail_supported(d, f) || heads <= 0 || d % heads != 0) return 0;
+  const int hd = d / heads;
+  if (d == 32 && f == 32) return attn_tail_fits_hd<32, 32>(hd);
+  if (d == 32 && f == 64) return attn_tail_fits_hd<32, 64>(hd);
+  if (d == 32 && f == 128) return attn_tail_fits_hd<32, 128>(hd);
+  if (d == 64 && f == 64) return attn_tail_fits_hd<64, 64>(hd);
+  if (d == 64 && f == 128) return attn_tail_fits_hd<64, 128>(hd);
+  if (d == 64 && f == 256) return attn_tail_fits_hd<64, 256>(hd);
+  return attn_tail_fits_hd<128, 128>(hd);
 }
 
 extern "C" int32_t mpk_attention_layer_tail_rows(void) { return kAttnTailRows; }
@@ -1084,13 +1197,14 @@ extern "C" int mpk_attention_layer_tail(const void* qkv_in, const float* x, cons
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool L = last != 0;
   hipError_t e;
-  if (d == 32 && f == 32) e = attn_tail_launch<32, 32>(L, a, s);
-  else if (d == 32 && f == 64) e = attn_tail_launch<32, 64>(L, a, s);
-  else if (d == 32 && f == 128) e = attn_tail_launch<32, 128>(L, a, s);
-  else if (d == 64 && f == 64) e = attn_tail_launch<64, 64>(L, a, s);
-  else if (d == 64 && f == 128) e = attn_tail_launch<64, 128>(L, a, s);
-  else if (d == 64 && f == 256) e = attn_tail_launch<64, 256>(L, a, s);
-  else e = attn_tail_launch<128, 128>(L, a, s);
+  const int hd = d / heads;
+  if (d == 32 && f == 32) e = attn_tail_launch<32, 32>(hd, L, a, s);
+  else if (d == 32 && f == 64) e = attn_tail_launch<32, 64>(hd, L, a, s);
+  else if (d == 32 && f == 128) e = attn_tail_launch<32, 128>(hd, L, a, s);
+  else if (d == 64 && f == 64) e = attn_tail_launch<64, 64>(hd, L, a, s);
+  else if (d == 64 && f == 128) e = attn_tail_launch<64, 128>(hd, L, a, s);
+  else if (d == 64 && f == 256) e = attn_tail_launch<64, 256>(hd, L, a, s);
+  else e = attn_tail_launch<128, 128>(hd, L, a, s);
   return (int)e;
 }
 

@@ -202,6 +202,18 @@ __device__ __forceinline__ void store8(_Float16* p, const float* v) {
 // VALU operations.  Over x in [-12, 12] the result differs from the float64 GELU
 // by at most 3.4e-7 (FP32 emulation of these steps), below the rounding error of
 // evaluating 0.5 x (1 + erff(x / sqrt 2)) in FP32 (4.5e-7).
+// Pin an FP32 value in a register (an empty asm), so that a later conversion to FP16 rounds
+// this FP32 value: otherwise the compiler may fuse the producing multiply or FMA and the
+// conversion into v_fma_mix, which rounds the exact result once - in some kernel
+// instantiations and not in others, so the same arithmetic would round differently
+// depending on the tile shape.  The reference rounds its FP32 results, then casts.
+__device__ __forceinline__ void pin_f32(float& x) { __asm__("" : "+v"(x)); }
+// the same for four / eight values in one statement (fewer scheduling boundaries)
+__device__ __forceinline__ void pin_f32x4(float* x) { __asm__("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3])); }
+__device__ __forceinline__ void pin_f32x8(float* x) {
+  __asm__("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7]));
+}
+
 __device__ __forceinline__ float gelu_erf(float x) {
   constexpr float kU = 0.84932180028801904f;  // sqrt(log2 e) / sqrt 2
   constexpr float kP = 0.2727374808792225f;   // 0.3275911 / sqrt(log2 e)

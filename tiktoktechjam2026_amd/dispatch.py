@@ -80,19 +80,30 @@ ATTENTION_HEAD_DIMS = (8, 16, 32, 64, 128, 256)
 # must equal mpk_layer_tail_supported / mpk_layernorm_qkv_supported in the library.
 LAYER_TAIL_SHAPES = frozenset({(32, 32), (32, 64), (32, 128), (64, 64), (64, 128), (64, 256), (128, 128)})
 LAYERNORM_QKV_WIDTHS = frozenset({32, 64, 128})
-# Attention inside the layer-tail kernel (head dim 32; must equal
-# mpk_attention_layer_tail_supported): one launch per layer for short sequences made of whole
-# 64-row tiles, without a key mask.
-ATTENTION_TAIL_SHAPES = frozenset(s for s in LAYER_TAIL_SHAPES if s[0] % 32 == 0)
+# Attention inside the layer-tail kernel: one launch per layer for short sequences made of
+# whole 64-row tiles, without a key mask.  Head dim 32 on every tail shape, head dim 16 on
+# d_model 32 and 64 (attention_tail_supported must equal mpk_attention_layer_tail_supported).
 ATTENTION_TAIL_ROWS = 64
-# Where the route uses it (whole forwards, HIP-graph replay on MI355X, fused vs separate
-# attention + tail): d_model 32 is 18-20 % faster up to 256 positions, d_model 64 10-17 %;
-# at 512 positions d_model 64 is 40 % slower (a workgroup's 64 rows then walk 8 key tiles
-# with one wave per SIMD, where the attention kernel spreads them over many CUs), and
-# d_model 128 is slower at every length (2-4 % at 128 positions: its register-resident QKV
-# weights and four heads' softmax state exceed the VGPRs, the rest goes to AGPRs).
-ATTENTION_TAIL_ROUTE_WIDTHS = frozenset({32, 64})
-ATTENTION_TAIL_MAX_SEQ = 256
+# Where the route uses it: the longest sequence per (d_model, head dim), from whole forwards
+# timed fused vs separate attention + tail (HIP-graph replay on MI355X, one process):
+#   d_model 32, hd 32: -18 to -20 % at 128 and 256 positions
+#   d_model 64, hd 32: -10 to -17 % at 128 and 256; +40 % at 512 (a workgroup's 64 rows then
+#                      walk 8 key tiles with one wave per SIMD, where the attention kernel
+#                      spreads them over many CUs)
+#   d_model 32, hd 16: -10 to -13 % at 128, -6 to -10 % at 256 (cfg3), -3 to -5 % at 512
+#   d_model 64, hd 16: -6 to -9 % at 128; +4 to +9 % at 256
+#   d_model 128, hd 32: slower at every length (+2-4 % at 128 positions: its register-resident
+#                      QKV weights and four heads' softmax state exceed the VGPRs)
+ATTENTION_TAIL_ROUTE_MAX_SEQ = {(32, 32): 256, (64, 32): 256, (32, 16): 512, (64, 16): 128}
+
+
+def attention_tail_supported(d_model: int, ffn_dim: int, heads: int) -> bool:
+    """Shapes built into the fused attention + layer-tail kernel (``mpk_attention_layer_tail_supported``)."""
+    d, f, h = int(d_model), int(ffn_dim), int(heads)
+    if (d, f) not in LAYER_TAIL_SHAPES or h <= 0 or d % h:
+        return False
+    hd = d // h
+    return hd == 32 or (hd == 16 and d <= 64)
 # From this width up the out-projection and FFN run as GEMMs + a separate LayerNorm.
 WIDE_GEMM_FROM = 256
 # GEMM-route widths whose out-projection fuses the next LayerNorm (tiles holding whole
@@ -117,7 +128,8 @@ class Route:
     fuse_attention_output_norm: bool = True
     fuse_full_ffn: bool = True
     fuse_layer_tail: bool = False
-    fuse_attention_tail: bool = False  # head dim 32, d_model <= 64 on the layer-tail route: see attention_tail_for
+    fuse_attention_tail: bool = False  # attention inside the layer tail, up to attention_tail_max_seq positions
+    attention_tail_max_seq: int = 0
     wide_ln_epilogue: bool = False
     wide_ln_ffn_out: bool = False
     qkv_variant: int = 0
@@ -192,9 +204,10 @@ def plan(
         enable_attention_output_norm_fusion and enable_full_ffn_fusion and not narrow
         and d in WIDE_LN_EPILOGUE_WIDTHS
     )
-    fuse_attn_tail = (
-        fuse_tail and hd == 32 and (d, f) in ATTENTION_TAIL_SHAPES and d in ATTENTION_TAIL_ROUTE_WIDTHS
+    attn_tail_max_seq = (
+        ATTENTION_TAIL_ROUTE_MAX_SEQ.get((d, hd), 0) if fuse_tail and attention_tail_supported(d, f, h) else 0
     )
+    fuse_attn_tail = attn_tail_max_seq > 0
     route = Route(
         True,
         "hip",
@@ -204,6 +217,7 @@ def plan(
         fuse_full_ffn=fuse_ffn,
         fuse_layer_tail=fuse_tail,
         fuse_attention_tail=fuse_attn_tail,
+        attention_tail_max_seq=attn_tail_max_seq,
         wide_ln_epilogue=wide_ln,
         wide_ln_ffn_out=wide_ln and d in WIDE_LN_FFN_OUT_WIDTHS,
     )
@@ -212,10 +226,10 @@ def plan(
 
 def attention_tail_for(route: Route, seq_len: int, masked: bool) -> bool:
     """Whether a forward over ``seq_len`` positions runs attention inside the layer-tail kernel:
-    the route allows it (head dim 32, a supported tail shape, d_model in
-    ATTENTION_TAIL_ROUTE_WIDTHS), no key mask, and the sequence is whole 64-row tiles of at
-    most ATTENTION_TAIL_MAX_SEQ positions."""
+    the route allows it (a supported shape listed in ATTENTION_TAIL_ROUTE_MAX_SEQ), no key
+    mask, and the sequence is whole 64-row tiles of at most ``route.attention_tail_max_seq``
+    positions."""
     return (
-        route.fuse_attention_tail and not masked and 0 < seq_len <= ATTENTION_TAIL_MAX_SEQ
+        route.fuse_attention_tail and not masked and 0 < seq_len <= route.attention_tail_max_seq
         and seq_len % ATTENTION_TAIL_ROWS == 0
     )

@@ -1,8 +1,8 @@
 """Cross-operator fusions of the HIP forward (no single reference function corresponds).
 
-``fused_attention_layer_tail`` runs the causal (or full) attention of head dim 32 in the
-same kernel, from the packed QKV projection, for sequences whose length is a multiple of
-its 64-row tiles (no key mask): one launch per layer instead of two.
+``fused_attention_layer_tail`` runs the causal (or full) attention of head dim 32 (or 16 at
+d_model 32 and 64) in the same kernel, from the packed QKV projection, for sequences whose
+length is a multiple of its 64-row tiles (no key mask): one launch per layer instead of two.
 
 ``fused_layer_tail`` composes, with the same rounding points, the reference's
 ``mixed_linear_add_layer_norm`` (attention output projection + residual + LN2),
@@ -23,7 +23,7 @@ import torch
 import torch.nn as nn
 
 from .. import _ops
-from ..dispatch import ATTENTION_TAIL_ROWS, ATTENTION_TAIL_SHAPES, LAYER_TAIL_SHAPES, LAYERNORM_QKV_WIDTHS
+from ..dispatch import ATTENTION_TAIL_ROWS, LAYER_TAIL_SHAPES, LAYERNORM_QKV_WIDTHS, attention_tail_supported
 from .hip_linear import _fp16_linear_ok, _gpu, _norm_ok
 
 
@@ -103,10 +103,10 @@ def fused_layer_tail(
 
 def attention_layer_tail_supported(d_model: int, ffn_dim: int, heads: int, seq_len: int) -> bool:
     """Shapes of ``mpk_attention_layer_tail`` (``mpk_attention_layer_tail_supported`` and
-    ``_rows``; the tables are checked against the library by the tests): head dim 32, a
-    layer-tail shape whose LDS also holds the attention tiles, whole 64-row tiles."""
-    d, f, h, s = int(d_model), int(ffn_dim), int(heads), int(seq_len)
-    return (d, f) in ATTENTION_TAIL_SHAPES and h > 0 and d == 32 * h and s > 0 and s % ATTENTION_TAIL_ROWS == 0
+    ``_rows``; the tables are checked against the library by the tests): head dim 32 on a
+    layer-tail shape or 16 at d_model 32 / 64, whole 64-row tiles."""
+    s = int(seq_len)
+    return attention_tail_supported(d_model, ffn_dim, heads) and s > 0 and s % ATTENTION_TAIL_ROWS == 0
 
 
 def fused_attention_layer_tail(
@@ -125,7 +125,7 @@ def fused_attention_layer_tail(
     """Attention over this layer's packed ``qkv [B, S, 3D]`` (FP16) and everything after it up to
     the next layer's QKV projection, in one kernel.
 
-    Same arithmetic as ``attention`` (16x16 kernel, 64-key tiles) followed by
+    Same arithmetic as ``attention`` (variant 1: 16x16 kernel, 64-key tiles) followed by
     ``fused_layer_tail``.  Returns ``(residual_out, next qkv)``, or ``(residual_out,
     next_norm(residual_out))`` in FP32 when ``next_qkv_proj`` is None (last layer).
     """
