@@ -113,3 +113,24 @@ def test_parity_table_orders_records(tmp_path):
     assert "Kernels as of commit `abc1234`." in text
     rows = [ln for ln in text.splitlines() if ln.startswith("| cfg")][1:]  # after the header row
     assert rows[0].startswith("| cfg1 | 1 |") and rows[1].startswith("| cfg5 | 0 |")
+
+
+def test_fused_attention_tail_kernels_are_named_and_priced():
+    """cfg3 runs attention inside the layer tail: the cost model lists the fused kernels (each
+    reading the packed QKV instead of the context) and the trace names map to them."""
+    from tiktoktechjam2026_amd import profiling
+    from tiktoktechjam2026_amd.config import BENCHMARK_CONFIGS
+
+    cfg3 = BENCHMARK_CONFIGS["cfg3"]
+    costs = profiling.forward_costs(cfg3)
+    assert set(costs) == {"layernorm_qkv", "attention_layer_tail", "attention_layer_tail_last"}
+    m, d = cfg3.batch_size * cfg3.seq_len, cfg3.d_model
+    assert costs["attention_layer_tail"].launches_per_forward == cfg3.num_layers - 1
+    assert costs["attention_layer_tail"].bytes > m * d * 20 and costs["attention_layer_tail_last"].bytes > m * d * 18
+    cfg1 = profiling.forward_costs(BENCHMARK_CONFIGS["cfg1"])  # two-kernel route
+    assert "attention" in cfg1 and "layer_tail" in cfg1
+    key = profiling.base_kernel_key
+    assert key("_ZN3mpk17layer_tail_kernelILi32ELi64ELi1ELb1ELb0ELi1ELi4ELi16EEEvNS_8TailArgsE") == "attention_layer_tail"
+    assert key("_ZN3mpk17layer_tail_kernelILi32ELi64ELi1ELb1ELb1ELi1ELi4ELi32EEEvNS_8TailArgsE") == "attention_layer_tail_last"
+    assert key("_ZN3mpk17layer_tail_kernelILi128ELi128ELi1ELb1ELb0ELi2ELi4ELi0EEEvNS_8TailArgsE") == "layer_tail"
+    assert key("_ZN3mpk17layer_tail_kernelILi128ELi128ELi1ELb0ELb0ELi2ELi4ELi0EEEvNS_8TailArgsE") == "layernorm_qkv"

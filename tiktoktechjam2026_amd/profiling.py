@@ -67,6 +67,24 @@ def forward_costs(config, normalized_bytes: int = 2, route=None) -> Dict[str, Ke
     sn = normalized_bytes
     pairs = S * (S + 1) / 2 if config.causal else S * S
     attention = KernelCost("attention", L, 4.0 * B * H * hd * pairs, 8.0 * B * S * D)
+    if route.fuse_layer_tail and dispatch.attention_tail_for(route, S, masked=False):
+        # attention inside the tail: per token the packed QKV (6 D) and x (4 D) are read and
+        # x' (4 D) and the next QKV (6 D) - or the final normalized row (4 D) - written
+        w_tail = 2.0 * (D * D + 2 * D * F + 3 * D * D)
+        return {
+            "layernorm_qkv": KernelCost(
+                "layernorm_qkv", 1, 2.0 * M * 3 * D * D, M * D * 4 + M * 3 * D * 2 + 2.0 * 3 * D * D
+            ),
+            "attention_layer_tail": KernelCost(
+                "attention_layer_tail", L - 1,
+                attention.flops + 2.0 * M * D * D + 4.0 * M * D * F + 6.0 * M * D * D,
+                M * D * (6 + 4 + 4 + 6) + w_tail,
+            ),
+            "attention_layer_tail_last": KernelCost(
+                "attention_layer_tail_last", 1, attention.flops + 2.0 * M * D * D + 4.0 * M * D * F,
+                M * D * (6 + 4 + 4 + 4) + 2.0 * (D * D + 2 * D * F),
+            ),
+        }
     if route.fuse_layer_tail:
         w_tail = 2.0 * (D * D + 2 * D * F + 3 * D * D)
         return {
@@ -176,7 +194,7 @@ def _row(name: str, cost: KernelCost, seconds: float) -> Dict[str, object]:
 def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[Dict[str, object]]:
     """Time each distinct kernel of ``model``'s forward on input ``x`` (first layer's weights)."""
     from .custom_kernel.hip_attention import attention
-    from .mixed_precision.hip_fused import fused_layer_tail, layer_norm_qkv
+    from .mixed_precision.hip_fused import fused_attention_layer_tail, fused_layer_tail, layer_norm_qkv
     from .mixed_precision.hip_linear import (
         layer_norm, mixed_ffn_add_layer_norm, mixed_linear, mixed_linear_add_layer_norm, mixed_linear_residual,
         mixed_linear_residual_layer_norm,
@@ -193,8 +211,21 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
     sdt = route.normalized_dtype
     causal = bool(config.causal)
     costs = forward_costs(config, 2 if sdt == torch.float16 else 4, route)
+    from . import dispatch
+
     with torch.inference_mode():
-        if route.fuse_layer_tail:
+        if route.fuse_layer_tail and dispatch.attention_tail_for(route, S, masked=False):
+            qkv = layer_norm_qkv(x, layer.norm1, att.qkv_proj, variant=route.head_variant)
+            launches = {
+                "layernorm_qkv": lambda: layer_norm_qkv(x, layer.norm1, att.qkv_proj, variant=route.head_variant),
+                "attention_layer_tail": lambda: fused_attention_layer_tail(
+                    qkv, x, att.num_heads, att.scale, causal, att.out_proj, layer.norm2, layer.ffn_in, layer.ffn_out,
+                    layer.norm1, att.qkv_proj),
+                "attention_layer_tail_last": lambda: fused_attention_layer_tail(
+                    qkv, x, att.num_heads, att.scale, causal, att.out_proj, layer.norm2, layer.ffn_in, layer.ffn_out,
+                    model.final_norm, None),
+            }
+        elif route.fuse_layer_tail:
             qkv = layer_norm_qkv(x, layer.norm1, att.qkv_proj, variant=route.head_variant)
             q, k, v = qkv.view(B, S, 3, att.num_heads, att.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
             ctx = attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant).view(B, S, D)
@@ -336,7 +367,9 @@ def base_kernel_key(name: str) -> str:
     if base == "layer_tail_kernel" and len(args) >= 5:
         if args[3] == "false":
             return "layernorm_qkv"
-        return "layer_tail_last" if args[4] == "true" else "layer_tail"
+        # layer_tail_kernel<D, F, TM, STAGE1, LAST, QMODE, W, AHD>: AHD > 0 computes attention too
+        attn = "attention_" if len(args) >= 8 and args[7] not in ("0", "") else ""
+        return attn + ("layer_tail_last" if args[4] == "true" else "layer_tail")
     if base in ("attention32_kernel", "attention_kernel"):
         return "attention"
     if base in ("linear_big_kernel", "linear_kernel"):
