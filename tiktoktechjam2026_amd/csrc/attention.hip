@@ -967,7 +967,9 @@ void attention32_kernel(AttnArgs a) {
       // Steady tiles: the weights are computed from the current row max first, and
       // the rescale test runs on them - a weight above 2^kRescaleLog2 means a score
       // above the max by more than kRescaleLog2 (an overflowing weight is +inf,
-      // which counts too) - as 3-input packed FP16 maxima over the weight registers,
+      // which counts too; FP16 rounding lets scores up to ~7e-4 above the threshold
+      // pass, where the score test below would fire - both keep o = acc / l exact) -
+      // as 3-input packed FP16 maxima over the weight registers,
       // NB * 4 instructions instead of the 16 NB FP32 ones over the scores.  Only
       // when it fires (rarely once a row has seen its first keys) are the scores
       // computed again (the K tile is still in LDS; keeping them would cost the
