@@ -59,6 +59,16 @@ int mpk_layernorm(const float* x, const float* update, const float* gamma, const
  */
 int mpk_linear(const void* x, int x_dtype, const void* w, const void* b, void* y, int y_dtype, int gelu,
                int64_t m, int32_t n, int32_t k, int variant, void* stream);
+
+/*
+ * mpk_linear without GELU, with output columns [0, q_cols) multiplied by q_scale in FP32 before
+ * the output rounding: the packed QKV projection with the attention's scale * log2(e) folded
+ * into q, for mpk_causal_attention_prescaled.  q_cols % 8 == 0, 0 <= q_cols <= n.
+ * No single reference counterpart: the reference scales the scores instead
+ * (custom_kernel/triton_attention.py:85, after mixed_linear at mixed_precision/transformer.py:88-120).
+ */
+int mpk_linear_qscaled(const void* x, int x_dtype, const void* w, const void* b, void* y, int y_dtype, int64_t m,
+                       int32_t n, int32_t k, int32_t q_cols, float q_scale, int variant, void* stream);
 int mpk_linear_auto_variant(int64_t m, int32_t n, int32_t k);
 
 /*
@@ -145,6 +155,18 @@ int mpk_causal_attention(const void* q, const void* k, const void* v, void* o, i
                          int32_t head_dim, float scale, int causal, const uint8_t* key_valid, int variant,
                          void* stream);
 int mpk_attention_auto_variant(int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim);
+
+/*
+ * mpk_causal_attention for FP16 q / k / v whose q already holds q * scale * log2(e), rounded to
+ * FP16 once by its producer (mpk_linear_qscaled): the 32x32 kernel (head_dim 32 or 64, variant 0
+ * or 6-8) with the scores already in log2 units, so no per-score scaling.  out_dtype kF16 or kF32.
+ * Replaces, with the scale moved into the projection: fp16_causal_attention
+ * (custom_kernel/triton_attention.py:341-390).
+ */
+int mpk_causal_attention_prescaled(const void* q, const void* k, const void* v, void* o, int out_dtype,
+                                   const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                                   const int64_t* o_strides, int32_t batch, int32_t heads, int32_t seq_len,
+                                   int32_t head_dim, int causal, const uint8_t* key_valid, int variant, void* stream);
 
 /*
  * Whole-layer tail for narrow models: everything after attention up to the next

@@ -28,6 +28,10 @@ ROUTES = {
     "gemm_ln_epilogue_d256": (TransformerConfig(2, 64, 256, 8, 1024, 2, True),
                               {"mpk.layer_norm.default": 1, "mpk.attention.default": 2}),
     "gemm_d512": (TransformerConfig(2, 64, 512, 8, 2048, 2, True), {"mpk.attention.default": 2}),
+    # head dim 32 from 256 positions: q leaves the projection pre-scaled, the attention skips the scale
+    "gemm_prescaled_d256": (TransformerConfig(1, 256, 256, 8, 1024, 2, True),
+                            {"mpk.linear_qscaled.default": 2, "mpk.attention_prescaled.default": 2,
+                             "mpk.attention.default": 0}),
     "row_fused_d96": (TransformerConfig(2, 64, 96, 3, 192, 2, True), {"mpk.attention.default": 2}),
 }
 

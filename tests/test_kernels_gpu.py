@@ -750,3 +750,72 @@ def test_attention_layer_tail_rejects(hip_device):
         _lib.stream_handle(qkv.device),
     )
     assert status == _lib.MPK_EINVAL
+
+
+# --------------------------------------------------------------------------- pre-scaled q
+
+
+@pytest.mark.parametrize("m,n,k,q_cols", [(130, 768, 256, 256), (8192, 384, 128, 128), (257, 40, 24, 16), (64, 96, 32, 0)])
+@pytest.mark.parametrize("variant", [0, 1, 5, 7, 8])
+def test_linear_q_scaled(hip_device, m, n, k, q_cols, variant):
+    """The QKV projection with the attention scale folded into q: columns from q_cols on equal
+    mpk_linear's bit for bit (the same kernel, times 1), the first q_cols are (x W^T + b) * c
+    rounded to FP16 once."""
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear, mixed_linear_q_scaled
+
+    x = _randn((m, k), 91, 1.0).to(hip_device, torch.float16)
+    lin = _linear(k, n, hip_device, 92)
+    c = 0.25503486
+    y = mixed_linear_q_scaled(x, lin, q_cols, c, variant=variant)
+    plain = mixed_linear(x, lin, output_dtype=torch.float16, variant=variant)
+    assert y.dtype == torch.float16 and y.shape == (m, n)
+    assert torch.equal(y[:, q_cols:], plain[:, q_cols:])
+    if q_cols:
+        ref = _ref_linear(x, lin, False)[:, :q_cols] * c
+        err = (y[:, :q_cols].cpu().double() - ref).abs()
+        assert float((err / ref.abs().clamp_min(1e-3)).max()) < 2e-3, float(err.max())
+
+
+@pytest.mark.parametrize(
+    "b,h,s,hd", [(2, 4, 256, 32), (1, 8, 300, 64), (3, 4, 1024, 32), (1, 2, 4096, 32), (2, 2, 33, 32), (1, 3, 517, 64)]
+)
+@pytest.mark.parametrize("variant", [0, 6, 7, 8])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_prescaled(hip_device, b, h, s, hd, variant, causal):
+    """attention_prescaled over q * scale * log2(e) (rounded to FP16 once) against the float64
+    reference of the unscaled problem, with and without a key mask."""
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention_prescaled
+
+    qkv = _randn((b, s, 3, h, hd), 97, 1.5)
+    scale = hd ** -0.5
+    c = float(torch.tensor(scale, dtype=torch.float32) * torch.tensor(1.4426950408889634, dtype=torch.float32))
+    qkv_ps = qkv.clone()
+    qkv_ps[:, :, 0] *= c
+    qkv16, qkv_ps16 = qkv.to(hip_device, torch.float16), qkv_ps.to(hip_device, torch.float16)
+    q, k, v = qkv16.permute(2, 0, 3, 1, 4).unbind(0)
+    qs = qkv_ps16.permute(2, 0, 3, 1, 4)[0]
+    out = attention_prescaled(qs, k, v, causal=causal, variant=variant)
+    assert out.shape == (b, s, h, hd) and out.dtype == torch.float16 and out.is_contiguous()
+    # the reference takes the unscaled q in FP32 (its FP16 rounding differs from that of q c)
+    ref = _ref_attention(qkv[:, :, 0].permute(0, 2, 1, 3).float(), k, v, scale, causal)
+    _close(out, ref, 4e-3, 4e-3, "pre-scaled attention")
+    lengths = torch.tensor([max(1, s - 29 * (i + 1)) for i in range(b)])
+    key_valid = (torch.arange(s)[None, :] < lengths[:, None]).to(hip_device)
+    out_m = attention_prescaled(qs, k, v, causal=causal, key_valid=key_valid, variant=variant)
+    ref_m = _ref_attention(qkv[:, :, 0].permute(0, 2, 1, 3).float(), k, v, scale, causal, key_valid)
+    rows = torch.isfinite(ref_m).all(dim=-1)
+    _close(out_m.cpu()[rows], ref_m[rows], 4e-3, 4e-3, "pre-scaled attention, key mask")
+
+
+def test_attention_prescaled_rejects(hip_device):
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention_prescaled
+
+    _, q, k, v = _packed_qkv(1, 64, 2, 16, 5, hip_device, torch.float16)
+    with pytest.raises(ValueError):
+        attention_prescaled(q, k, v)  # head dim 16: the 16x16 kernel has no pre-scaled form
+    _, q, k, v = _packed_qkv(1, 64, 2, 32, 5, hip_device, torch.float16)
+    with pytest.raises(ValueError):
+        attention_prescaled(q, k, v, variant=1)
+    _, q, k, v = _packed_qkv(1, 64, 2, 32, 5, hip_device, torch.float32)
+    with pytest.raises(ValueError):
+        attention_prescaled(q, k, v)

@@ -45,6 +45,13 @@ SIGNATURES = {
         [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_i64, _c_i32, _c_i32, _c_int, _c_void_p],
     ),
     "mpk_linear_auto_variant": (_c_int, [_c_i64, _c_i32, _c_i32]),
+    "mpk_linear_qscaled": (
+        _c_int,
+        [
+            _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i32, _c_i32, _c_i32, _c_float,
+            _c_int, _c_void_p,
+        ],
+    ),
     "mpk_linear_residual": (
         _c_int,
         [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i32, _c_i32, _c_int, _c_void_p],
@@ -80,6 +87,13 @@ SIGNATURES = {
         ],
     ),
     "mpk_attention_auto_variant": (_c_int, [_c_i32, _c_i32, _c_i32, _c_i32]),
+    "mpk_causal_attention_prescaled": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64_p, _c_i64_p, _c_i64_p, _c_i64_p,
+            _c_i32, _c_i32, _c_i32, _c_i32, _c_int, _c_void_p, _c_int, _c_void_p,
+        ],
+    ),
     "mpk_layer_tail": (
         _c_int,
         [

@@ -122,6 +122,31 @@ def _(x, weight, bias, out_dtype, gelu, variant):
     return x.new_empty((*x.shape[:-1], weight.shape[0]), dtype=_dtype(out_dtype))
 
 
+@torch.library.custom_op("mpk::linear_qscaled", mutates_args=())
+def linear_qscaled(
+    x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, out_dtype: int, q_cols: int, q_scale: float,
+    variant: int,
+) -> torch.Tensor:
+    """``fp16(x) W^T + b`` with columns below ``q_cols`` multiplied by ``q_scale`` before the
+    output rounding (``mpk_linear_qscaled``)."""
+    n, k = weight.shape
+    out = torch.empty((*x.shape[:-1], n), device=x.device, dtype=_dtype(out_dtype))
+    _require_aligned("unsupported mixed projection inputs", x, weight, bias, out)
+    _lib.check(
+        _lib.load().mpk_linear_qscaled(
+            x.data_ptr(), _lib.dtype_code(x.dtype), weight.data_ptr(), bias.data_ptr(), out.data_ptr(),
+            int(out_dtype), _rows(x, k), n, k, int(q_cols), float(q_scale), int(variant), _lib.stream_handle(x.device),
+        ),
+        "mpk_linear_qscaled",
+    )
+    return out
+
+
+@linear_qscaled.register_fake
+def _(x, weight, bias, out_dtype, q_cols, q_scale, variant):
+    return x.new_empty((*x.shape[:-1], weight.shape[0]), dtype=_dtype(out_dtype))
+
+
 def _launch_linear_residual(x, weight, bias, residual, out, variant) -> None:
     n, k = weight.shape
     _require_aligned("unsupported mixed projection/residual inputs", x, weight, bias, residual, out)
@@ -321,6 +346,35 @@ def attention(
 
 @attention.register_fake
 def _(q, k, v, key_valid, scale, causal, out_dtype, variant):
+    batch, heads, seq_len, head_dim = q.shape
+    return q.new_empty((batch, seq_len, heads, head_dim), dtype=_dtype(out_dtype))
+
+
+@torch.library.custom_op("mpk::attention_prescaled", mutates_args=())
+def attention_prescaled(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_valid: Optional[torch.Tensor], causal: bool,
+    out_dtype: int, variant: int,
+) -> torch.Tensor:
+    """Flash attention over FP16 views whose q already holds q * scale * log2(e)
+    (``mpk_causal_attention_prescaled``) -> contiguous ``[B, S, H, hd]``."""
+    batch, heads, seq_len, head_dim = q.shape
+    _require_aligned(f"unsupported custom-attention input: shape={tuple(q.shape)}, dtype={q.dtype}", q, k, v)
+    out = torch.empty((batch, seq_len, heads, head_dim), device=q.device, dtype=_dtype(out_dtype))
+    o_strides = (out.stride(0), out.stride(2), out.stride(1), out.stride(3))
+    _lib.check(
+        _lib.load().mpk_causal_attention_prescaled(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), int(out_dtype),
+            _lib.strides4(q.stride()), _lib.strides4(k.stride()), _lib.strides4(v.stride()), _lib.strides4(o_strides),
+            batch, heads, seq_len, head_dim, 1 if causal else 0, _ptr(key_valid), int(variant),
+            _lib.stream_handle(q.device),
+        ),
+        "mpk_causal_attention_prescaled",
+    )
+    return out
+
+
+@attention_prescaled.register_fake
+def _(q, k, v, key_valid, causal, out_dtype, variant):
     batch, heads, seq_len, head_dim = q.shape
     return q.new_empty((batch, seq_len, heads, head_dim), dtype=_dtype(out_dtype))
 

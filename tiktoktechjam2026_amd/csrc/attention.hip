@@ -622,12 +622,16 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 // it the binding unit at these head dims.  Row sums of fp16(P) come from a 16x16x32 product with a 0/1
 // A operand (rows 0 and 1 pick the queries i and i + 16 out of the P fragment
 // layout), so l sums exactly the FP16 weights that multiply V.
-template <int HD, int NW, int KTILE, typename IT, typename OT, bool KEYMASK>
+// PS: q arrives pre-multiplied by scale * log2(e) (mpk_causal_attention_prescaled), so the
+// scores are already in log2 units: c = 1, and on steady tiles the S^T accumulator starts at
+// -m, which leaves p = 2^(acc) with no per-score FMA.
+template <int HD, int NW, int KTILE, typename IT, typename OT, bool KEYMASK, bool PS = false>
 // (four waves per SIMD, i.e. at most 128 VGPRs, for FP16 input at head dim 32 with 64-key
 // tiles; FP32 input carries a per-row score factor, one register more, and runs at three)
 __global__ __launch_bounds__(64 * NW) __attribute__((
     amdgpu_waves_per_eu(HD == 32 && KTILE == 64 && std::is_same<IT, _Float16>::value ? 4 : 1)))
 void attention32_kernel(AttnArgs a) {
+  static_assert(!PS || std::is_same<IT, _Float16>::value, "pre-scaled q is FP16");
   constexpr int NT = 64 * NW;
   using SH = AttnShape<HD, KTILE, NT>;
   constexpr int QB = 32 * NW;     // queries per workgroup, 32 per wave
@@ -711,8 +715,8 @@ void attention32_kernel(AttnArgs a) {
   // Q fragments (B operand of S^T): query q, head dims 16 st + 8 hf .. +7; negated for a
   // negative scale, so scores map to the exponent as fma(s, |c|, -m).  FP32 inputs: q' =
   // fp16(q 2^-a) for the row's exponent a, and c becomes |c| 2^(a + kexp).
-  float c = fabsf(a.c);
-  const bool neg = a.c < 0.f;
+  float c = PS ? 1.0f : fabsf(a.c);
+  const bool neg = !PS && a.c < 0.f;
   h8 qf[QS];
   if constexpr (F32IN) {
     // two passes over the row (the maximum first, then the scaled conversion), so no
@@ -870,13 +874,15 @@ void attention32_kernel(AttnArgs a) {
     if (EDGE && nbv <= 0) return;
     const bool need_bias = KEYMASK || kb + KTILE > S;
 
-    // S^T (32 keys x 32 queries) per block, raw scores
+    // S^T (32 keys x 32 queries) per block, raw scores (pre-scaled steady tiles: minus m)
+    constexpr bool STEADY = !EDGE && !MAYBE_FRESH && HD == 32 && KTILE == 64;
+    const float sc0 = (PS && STEADY) ? -mrow : 0.f;
     f16v sc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       if (EDGE && nb >= nbv) break;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sc[nb][e] = 0.f;
+      for (int e = 0; e < 16; ++e) sc[nb][e] = sc0;
 #pragma unroll
       for (int st = 0; st < QS; ++st) {
         const h8 ka = *reinterpret_cast<const h8*>(&ksb[(32 * nb + trow) * SH::LDK + 16 * st + 8 * hf]);
@@ -963,7 +969,7 @@ void attention32_kernel(AttnArgs a) {
 
     // (head dim 32 with 64-key tiles only: the tile's weights held at once cost a
     // wave per SIMD of occupancy at head dim 64 and with 128-key tiles)
-    if constexpr (!EDGE && !MAYBE_FRESH && HD == 32 && KTILE == 64) {
+    if constexpr (STEADY) {
       // Steady tiles: the weights are computed from the current row max first, and
       // the rescale test runs on them - a weight above 2^kRescaleLog2 means a score
       // above the max by more than kRescaleLog2 (an overflowing weight is +inf,
@@ -981,7 +987,14 @@ void attention32_kernel(AttnArgs a) {
       const h8 va0[2] = {vt_frag(vtb, 0, 8 * hf), vt_frag(vtb, 0, 16 + 8 * hf)};
       h8 pf[NB][2];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) weights(nb, pf[nb]);
+      for (int nb = 0; nb < NB; ++nb) {
+        if constexpr (PS) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) pf[nb][e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(sc[nb][e]);
+        } else {
+          weights(nb, pf[nb]);
+        }
+      }
       typedef _Float16 h2v __attribute__((ext_vector_type(2)));
       auto pair = [&](int k) {  // packed weight pair k of the tile (NB * 8 pairs, one register each)
         const h8 v = pf[k >> 3][(k >> 2) & 1];
@@ -1118,7 +1131,7 @@ void attention32_kernel(AttnArgs a) {
   }
 }
 
-template <int HD, int NW, int KTILE, typename IT, typename OT>
+template <int HD, int NW, int KTILE, typename IT, typename OT, bool PS = false>
 static hipError_t launch_attn32(const AttnArgs& a0, hipStream_t s) {
   constexpr int QB = 32 * NW;
   const int64_t nqb = (a0.seq + QB - 1) / QB;
@@ -1132,9 +1145,11 @@ static hipError_t launch_attn32(const AttnArgs& a0, hipStream_t s) {
   a.group = (rows % 64 == 0 && (rows / 8) * nqb >= 1024) ? 8 : 0;
   if (grid > 0x7fffffff) return hipErrorInvalidConfiguration;
   if (a.key_valid)
-    hipLaunchKernelGGL((attention32_kernel<HD, NW, KTILE, IT, OT, true>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a);
+    hipLaunchKernelGGL((attention32_kernel<HD, NW, KTILE, IT, OT, true, PS>), dim3((unsigned)grid), dim3(64 * NW), 0, s,
+                       a);
   else
-    hipLaunchKernelGGL((attention32_kernel<HD, NW, KTILE, IT, OT, false>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a);
+    hipLaunchKernelGGL((attention32_kernel<HD, NW, KTILE, IT, OT, false, PS>), dim3((unsigned)grid), dim3(64 * NW), 0,
+                       s, a);
   return hipGetLastError();
 }
 
@@ -1179,12 +1194,12 @@ static hipError_t attn_variant_256(int variant, const AttnArgs& a, hipStream_t s
 }
 
 // 32x32 variants (head_dim 32 and 64): 6: 4 waves x 64-key tiles  7: 8 waves x 64  8: 4 waves x 128
-template <int HD, typename IT, typename OT>
+template <int HD, typename IT, typename OT, bool PS = false>
 static hipError_t attn32_variant(int variant, const AttnArgs& a, hipStream_t s) {
   switch (variant) {
-    case 6: return launch_attn32<HD, 4, 64, IT, OT>(a, s);
-    case 7: return launch_attn32<HD, 8, 64, IT, OT>(a, s);
-    case 8: return launch_attn32<HD, 4, 128, IT, OT>(a, s);
+    case 6: return launch_attn32<HD, 4, 64, IT, OT, PS>(a, s);
+    case 7: return launch_attn32<HD, 8, 64, IT, OT, PS>(a, s);
+    case 8: return launch_attn32<HD, 4, 128, IT, OT, PS>(a, s);
     default: return (hipError_t)MPK_EUNSUPPORTED;
   }
 }
@@ -1264,5 +1279,48 @@ extern "C" int mpk_causal_attention(const void* q, const void* k, const void* v,
   else
     e = out_dtype == kF16 ? attn_dispatch<float, _Float16>(variant, a, head_dim, s)
                           : attn_dispatch<float, float>(variant, a, head_dim, s);
+  return (int)e;
+}
+
+// q pre-multiplied by scale * log2(e) in FP32 and rounded to FP16 by its producer
+// (mpk_linear_qscaled): the 32x32 kernel (head dims 32 and 64, FP16 q / k / v) without the
+// per-score scale.  variant 0 picks among 6-8 as mpk_attention_auto_variant does from 256 keys.
+extern "C" int mpk_causal_attention_prescaled(const void* q, const void* k, const void* v, void* o, int out_dtype,
+                                              const int64_t* q_strides, const int64_t* k_strides,
+                                              const int64_t* v_strides, const int64_t* o_strides, int32_t batch,
+                                              int32_t heads, int32_t seq_len, int32_t head_dim, int causal,
+                                              const uint8_t* key_valid, int variant, void* stream) {
+  if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return MPK_EINVAL;
+  if (batch < 0 || heads <= 0 || seq_len < 0) return MPK_EINVAL;
+  if (out_dtype != kF32 && out_dtype != kF16) return MPK_EINVAL;
+  if (head_dim != 32 && head_dim != 64) return MPK_EUNSUPPORTED;
+  if (variant == 0) variant = head_dim == 32 ? (seq_len >= 4096 ? 7 : 6) : (seq_len < 1024 ? 7 : 6);
+  if (variant < 6 || variant > 8) return MPK_EUNSUPPORTED;
+  const int64_t* st[4] = {q_strides, k_strides, v_strides, o_strides};
+  const void* base[4] = {q, k, v, o};
+  for (int i = 0; i < 4; ++i) {
+    if (st[i][3] != 1) return MPK_EUNSUPPORTED;
+    const int esz = (i == 3 && out_dtype == kF32) ? 4 : 2;
+    if ((reinterpret_cast<uintptr_t>(base[i]) & 15u) != 0) return MPK_EALIGN;
+    for (int j = 0; j < 3; ++j)
+      if ((st[i][j] * esz) % 16 != 0) return MPK_EALIGN;
+  }
+  if (batch == 0 || seq_len == 0) return MPK_OK;
+  AttnArgs a{};
+  a.q = q; a.k = k; a.v = v; a.o = o;
+  for (int j = 0; j < 4; ++j) {
+    a.qs[j] = q_strides[j]; a.ks[j] = k_strides[j]; a.vs[j] = v_strides[j]; a.os[j] = o_strides[j];
+  }
+  a.key_valid = key_valid;
+  a.batch = batch; a.heads = heads; a.seq = seq_len; a.causal = causal ? 1 : 0;
+  a.c = 1.0f;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (head_dim == 32)
+    e = out_dtype == kF16 ? attn32_variant<32, _Float16, _Float16, true>(variant, a, s)
+                          : attn32_variant<32, _Float16, float, true>(variant, a, s);
+  else
+    e = out_dtype == kF16 ? attn32_variant<64, _Float16, _Float16, true>(variant, a, s)
+                          : attn32_variant<64, _Float16, float, true>(variant, a, s);
   return (int)e;
 }

@@ -46,7 +46,21 @@ struct LinearArgs {
   int n;
   int k;
   float eps;
+  // bias epilogue only (mpk_linear_qscaled): columns below q_cols are multiplied by q_scale
+  // in FP32 before the output rounding (the attention's scale * log2(e) folded into q)
+  int q_cols;
+  float q_scale;
 };
+
+// The q_cols / q_scale multiply of a bias epilogue on the 8 outputs at column n (a run of 8
+// never straddles q_cols, a multiple of 8); a scalar branch when the call scales nothing.
+__device__ __forceinline__ void q_scale8(const LinearArgs& a, int n, float* v) {
+  if (a.q_cols > 0) {
+    const float s = n < a.q_cols ? a.q_scale : 1.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] *= s;
+  }
+}
 
 template <int BM, int BN, int KC, int WAVES_M, typename XT, int EPI, typename OT>
 __global__ __launch_bounds__(kBlock) void linear_kernel(LinearArgs a) {
@@ -144,6 +158,7 @@ __global__ __launch_bounds__(kBlock) void linear_kernel(LinearArgs a) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) v[j] = gelu_erf(v[j]);
         }
+        if constexpr (EPI == kEpiBias) q_scale8(a, n, v);
         if constexpr (EPI == kEpiBiasResidual) {
           float rv[8];
           load8_f32(a.residual + m * N + n, rv);
@@ -478,6 +493,7 @@ __global__ __launch_bounds__(BM / 2 * BN / 64) void linear_big_kernel(LinearArgs
 #pragma unroll
           for (int j = 0; j < 8; ++j) v[j] = gelu_erf(v[j]);
         }
+        if constexpr (EPI == kEpiBias) q_scale8(a, n, v);
         if constexpr (EPI == kEpiBiasResidual) {
           float rv[8];
           load8_f32(a.residual + m * N + n, rv);
@@ -726,6 +742,7 @@ __global__ __launch_bounds__(512) void linear_dma_kernel(LinearArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = gelu_erf(v[j]);
       }
+      if constexpr (EPI == kEpiBias) q_scale8(a, n, v);
       if constexpr (EPI == kEpiBiasResidual) {
         typedef float v4 __attribute__((ext_vector_type(4)));
         const uint32_t ro = ok ? e * 4u : 0x80000000u;
@@ -943,6 +960,29 @@ extern "C" int mpk_linear(const void* x, int x_dtype, const void* w, const void*
     else e = yf ? linear_variant<_Float16, kEpiBias, float>(variant, a, s)
                 : linear_variant<_Float16, kEpiBias, _Float16>(variant, a, s);
   }
+  return (int)e;
+}
+
+extern "C" int mpk_linear_qscaled(const void* x, int x_dtype, const void* w, const void* b, void* y, int y_dtype,
+                                  int64_t m, int32_t n, int32_t k, int32_t q_cols, float q_scale, int variant,
+                                  void* stream) {
+  if (!x || !w || !b || !y || m < 0 || n <= 0 || k <= 0 || q_cols < 0 || q_cols > n) return MPK_EINVAL;
+  if ((x_dtype != kF32 && x_dtype != kF16) || (y_dtype != kF32 && y_dtype != kF16)) return MPK_EINVAL;
+  if (n % 8 != 0 || k % 8 != 0 || q_cols % 8 != 0) return MPK_EUNSUPPORTED;
+  if (!aligned16(x) || !aligned16(w) || !aligned16(b) || !aligned16(y)) return MPK_EALIGN;
+  if (m == 0) return MPK_OK;
+  if (variant == 0) variant = mpk_linear_auto_variant(m, n, k);
+  LinearArgs a{};
+  a.x = x; a.w = static_cast<const _Float16*>(w); a.bias = static_cast<const _Float16*>(b); a.y = y;
+  a.m = m; a.n = n; a.k = k;
+  a.q_cols = q_cols; a.q_scale = q_scale;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  const bool xf = x_dtype == kF32, yf = y_dtype == kF32;
+  if (xf) e = yf ? linear_variant<float, kEpiBias, float>(variant, a, s)
+                 : linear_variant<float, kEpiBias, _Float16>(variant, a, s);
+  else e = yf ? linear_variant<_Float16, kEpiBias, float>(variant, a, s)
+              : linear_variant<_Float16, kEpiBias, _Float16>(variant, a, s);
   return (int)e;
 }
 

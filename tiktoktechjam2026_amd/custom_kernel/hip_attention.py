@@ -102,6 +102,31 @@ def attention(
                           int(variant))
 
 
+def attention_prescaled(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    causal: bool = True,
+    key_valid: Optional[torch.Tensor] = None,
+    variant: int = 0,
+) -> torch.Tensor:
+    """``attention`` for FP16 inputs whose q already holds ``q * scale * log2(e)`` (rounded to
+    FP16 once, by ``hip_linear.mixed_linear_q_scaled``): the 32x32 kernel (head dims 32 and
+    64; ``variant`` 0 or 6-8) without the per-score scale.  Output FP16 ``[B, S, H, hd]``."""
+    if not _layout_ok(q, k, v, q.dtype) or q.dtype != torch.float16 or q.shape[-1] not in (32, 64):
+        raise ValueError(f"unsupported pre-scaled attention input: shape={tuple(q.shape)}, dtype={q.dtype}")
+    if int(variant) not in (0, 6, 7, 8):
+        raise ValueError(f"pre-scaled attention runs variants 6-8 (got {variant})")
+    batch, heads, seq_len, head_dim = q.shape
+    mask_u8 = None
+    if key_valid is not None:
+        if key_valid.shape != (batch, seq_len) or key_valid.device != q.device:
+            raise ValueError("key_valid must be a [batch, seq_len] mask on the input device")
+        mask_u8 = key_valid.to(torch.uint8).contiguous()
+    return _ops.attention_prescaled(q, k, v, mask_u8, bool(causal), F16, int(variant))
+
+
 def launch_causal_attention(
     q: torch.Tensor,
     k: torch.Tensor,

@@ -130,6 +130,9 @@ class Route:
     fuse_layer_tail: bool = False
     fuse_attention_tail: bool = False  # attention inside the layer tail, up to attention_tail_max_seq positions
     attention_tail_max_seq: int = 0
+    # head dim 32 off the layer-tail route: from 256 keys the QKV projection folds the attention
+    # scale into q and the 32x32 attention kernel skips its per-score FMA (prescaled_attention_for)
+    prescale_q: bool = False
     wide_ln_epilogue: bool = False
     wide_ln_ffn_out: bool = False
     qkv_variant: int = 0
@@ -218,6 +221,7 @@ def plan(
         fuse_layer_tail=fuse_tail,
         fuse_attention_tail=fuse_attn_tail,
         attention_tail_max_seq=attn_tail_max_seq,
+        prescale_q=enable_fp16_custom_attention and not fuse_tail and hd == 32,
         wide_ln_epilogue=wide_ln,
         wide_ln_ffn_out=wide_ln and d in WIDE_LN_FFN_OUT_WIDTHS,
     )
@@ -232,4 +236,18 @@ def attention_tail_for(route: Route, seq_len: int, masked: bool) -> bool:
     return (
         route.fuse_attention_tail and not masked and 0 < seq_len <= route.attention_tail_max_seq
         and seq_len % ATTENTION_TAIL_ROWS == 0
+    )
+
+
+# Sequence length from which the built-in attention choice at head dim 32 is the 32x32 kernel
+# (mpk_attention_auto_variant), whose steady tiles the pre-scaled q makes cheaper.
+PRESCALED_ATTENTION_MIN_SEQ = 256
+
+
+def prescaled_attention_for(route: Route, seq_len: int) -> bool:
+    """Whether a forward over ``seq_len`` positions projects q pre-multiplied by the attention's
+    scale * log2(e) and runs ``attention_prescaled`` (measured on MI355X: cfg5's attention
+    -6 %, 810 vs 862 us, from the per-score FMA it no longer needs; cfg2's -2 %)."""
+    return (
+        route.prescale_q and seq_len >= PRESCALED_ATTENTION_MIN_SEQ and route.attention_variant in (0, 6, 7, 8)
     )

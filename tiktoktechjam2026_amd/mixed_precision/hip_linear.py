@@ -89,6 +89,28 @@ def mixed_linear(
     return _ops.linear(x, linear.weight, linear.bias, _code(output_dtype), bool(fuse_gelu), int(variant))
 
 
+def mixed_linear_q_scaled(
+    x: torch.Tensor, linear: nn.Linear, q_cols: int, q_scale: float, *, variant: int = 0
+) -> torch.Tensor:
+    """``fp16(x) @ W^T + b`` -> FP16, with output columns below ``q_cols`` multiplied by
+    ``q_scale`` in FP32 before the FP16 rounding: the packed QKV projection with the attention's
+    ``scale * log2(e)`` folded into q, for ``attention_prescaled`` (no reference counterpart:
+    the reference scales the scores, ``custom_kernel/triton_attention.py:85``)."""
+    if not (
+        _gpu(x)
+        and x.dtype in (torch.float16, torch.float32)
+        and _fp16_linear_ok(linear)
+        and x.shape[-1] == linear.in_features
+        and linear.in_features % 8 == 0
+        and linear.out_features % 8 == 0
+        and 0 <= int(q_cols) <= linear.out_features
+        and int(q_cols) % 8 == 0
+    ):
+        raise ValueError("unsupported mixed projection inputs")
+    return _ops.linear_qscaled(x, linear.weight, linear.bias, _code(torch.float16), int(q_cols), float(q_scale),
+                               int(variant))
+
+
 def mixed_linear_residual(
     x: torch.Tensor,
     linear: nn.Linear,

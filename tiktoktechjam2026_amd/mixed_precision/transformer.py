@@ -41,20 +41,24 @@ from __future__ import annotations
 import copy
 from typing import Dict, Mapping, Optional, Union
 
+import numpy as np
 import torch
 import torch.nn as nn
 
 from .. import dispatch
-from ..custom_kernel.hip_attention import attention
+from ..custom_kernel.hip_attention import attention, attention_prescaled
 from .hip_fused import fused_attention_layer_tail, fused_layer_tail, layer_norm_qkv
 from .hip_linear import (
     layer_norm,
     mixed_ffn_add_layer_norm,
     mixed_linear,
     mixed_linear_add_layer_norm,
+    mixed_linear_q_scaled,
     mixed_linear_residual,
     mixed_linear_residual_layer_norm,
 )
+
+LOG2E = 1.4426950408889634
 
 
 class MixedPrecisionSelfAttention(nn.Module):
@@ -66,6 +70,9 @@ class MixedPrecisionSelfAttention(nn.Module):
         self.num_heads = num_heads
         self.head_dim = d_model // num_heads
         self.scale = self.head_dim ** -0.5
+        # scale * log2(e) as the attention kernels form it (an FP32 product): the factor a
+        # pre-scaled q carries (dispatch.prescaled_attention_for)
+        self.q_prescale = float(np.float32(self.scale) * np.float32(LOG2E))
         self.route = route
         self.qkv_proj = nn.Linear(d_model, 3 * d_model, bias=True)
         self.out_proj = nn.Linear(d_model, d_model, bias=True)
@@ -82,6 +89,15 @@ class MixedPrecisionSelfAttention(nn.Module):
     ) -> torch.Tensor:
         """QKV projection + flash attention -> context ``[B, S, D]`` (fp16, or fp32 on the fp32-I/O route)."""
         route = self.route
+        if dispatch.prescaled_attention_for(route, normalized.shape[1]):
+            # q leaves the projection multiplied by scale * log2(e) (one FP16 rounding, as q has
+            # without it), and the attention kernel needs no per-score scaling
+            qkv = mixed_linear_q_scaled(normalized, self.qkv_proj, self.d_model, self.q_prescale,
+                                        variant=route.qkv_variant)
+            batch, seq_len, _ = qkv.shape
+            q, k, v = qkv.view(batch, seq_len, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
+            ctx = attention_prescaled(q, k, v, causal=causal, key_valid=key_valid, variant=route.attention_variant)
+            return ctx.view(batch, seq_len, self.d_model)
         qkv_dtype = torch.float16 if route.fp16_attention else torch.float32
         qkv = mixed_linear(normalized, self.qkv_proj, output_dtype=qkv_dtype, variant=route.qkv_variant)
         return self.attend(qkv, key_valid, causal)
