@@ -881,8 +881,30 @@ void attention32_kernel(AttnArgs a) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       if (EDGE && nb >= nbv) break;
+      if constexpr (PS && STEADY) {
+        // -m into all 16 accumulator registers on every steady tile: one pair
+        // (-m, -m), then seven 64-bit moves instead of fifteen 32-bit ones (the
+        // compiler splats a scalar with 32-bit moves only; the immediate keeps the
+        // seven statements distinct so they are not merged into one).  The
+        // hazard recognizer counts an asm statement's outputs as VALU writes and
+        // puts the wait states an MFMA source needs after them.
+        typedef float f2v __attribute__((ext_vector_type(2)));
+        typedef double d8v __attribute__((ext_vector_type(8)));
+        const f2v pr = {sc0, sc0};
+        const double dp = __builtin_bit_cast(double, pr);
+        d8v dv;
+        dv[0] = dp;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sc[nb][e] = sc0;
+        for (int i = 1; i < 8; ++i) {
+          double t;
+          asm("v_mov_b64 %0, %1 ; %2" : "=v"(t) : "v"(dp), "n"(i));
+          dv[i] = t;
+        }
+        sc[nb] = __builtin_bit_cast(f16v, dv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sc[nb][e] = sc0;
+      }
 #pragma unroll
       for (int st = 0; st < QS; ++st) {
         const h8 ka = *reinterpret_cast<const h8*>(&ksb[(32 * nb + trow) * SH::LDK + 16 * st + 8 * hf]);

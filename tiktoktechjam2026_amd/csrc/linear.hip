@@ -54,11 +54,14 @@ struct LinearArgs {
 
 // The q_cols / q_scale multiply of a bias epilogue on the 8 outputs at column n (a run of 8
 // never straddles q_cols, a multiple of 8); a scalar branch when the call scales nothing.
+// The products are pinned as FP32 values, so the output conversion rounds them once more
+// to FP16 and cannot be fused with the multiply into one rounding (v_fma_mix).
 __device__ __forceinline__ void q_scale8(const LinearArgs& a, int n, float* v) {
   if (a.q_cols > 0) {
     const float s = n < a.q_cols ? a.q_scale : 1.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] *= s;
+    pin_f32x8(v);
   }
 }
 
