@@ -263,3 +263,41 @@ def test_attention_in_layer_tail_route_is_bit_identical(hip_device, causal, d, h
         model.route = dataclasses.replace(model.route, fuse_attention_tail=False)
         two = model(x)
     assert torch.equal(fused, two), (fused - two).abs().max().item()
+
+
+@pytest.mark.parametrize(
+    "d,heads,s,f,prescaled",
+    [(256, 8, 256, 512, True), (256, 8, 128, 512, False), (512, 8, 256, 1024, False), (128, 4, 256, 128, False)],
+)
+def test_kernel_table_times_the_route_kernels(hip_device, monkeypatch, d, heads, s, f, prescaled):
+    """bench.py's per-kernel table (profiling.forward_kernel_table) launches the kernels the
+    forward runs: the pre-scaled projection + attention pair where the route takes it (head dim
+    32 from 256 keys with a separate QKV launch), the scaled ones elsewhere; one row per kernel
+    the forward prices, each with a positive time."""
+    from tiktoktechjam2026_amd import dispatch, profiling
+    from tiktoktechjam2026_amd.custom_kernel import hip_attention
+    from tiktoktechjam2026_amd.mixed_precision import hip_linear
+
+    calls = {"attention": 0, "attention_prescaled": 0, "mixed_linear_q_scaled": 0}
+    for mod, name in ((hip_attention, "attention"), (hip_attention, "attention_prescaled"),
+                      (hip_linear, "mixed_linear_q_scaled")):
+        real = getattr(mod, name)
+
+        def counted(*args, _real=real, _name=name, **kwargs):
+            calls[_name] += 1
+            return _real(*args, **kwargs)
+
+        monkeypatch.setattr(mod, name, counted)
+    config = TransformerConfig(2, s, d, heads, f, 2, True)
+    _, model = _build(config, hip_device)
+    assert dispatch.prescaled_attention_for(model.route, s) == prescaled
+    x = torch.randn(2, s, d, generator=torch.Generator().manual_seed(4)).to(hip_device)
+    rows = profiling.forward_kernel_table(model, x, iterations=2)
+    costs = profiling.forward_costs(dataclasses.replace(config, batch_size=2), 2, model.route)
+    priced = {k for k, c in costs.items() if c.launches_per_forward > 0}
+    assert {r["kernel"] for r in rows} == priced
+    assert all(r["avg_us"] > 0 for r in rows)
+    if prescaled:
+        assert calls["attention_prescaled"] > 0 and calls["mixed_linear_q_scaled"] > 0 and calls["attention"] == 0
+    else:
+        assert calls["attention_prescaled"] == 0 and calls["mixed_linear_q_scaled"] == 0

@@ -193,11 +193,11 @@ def _row(name: str, cost: KernelCost, seconds: float) -> Dict[str, object]:
 
 def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[Dict[str, object]]:
     """Time each distinct kernel of ``model``'s forward on input ``x`` (first layer's weights)."""
-    from .custom_kernel.hip_attention import attention
+    from .custom_kernel.hip_attention import attention, attention_prescaled
     from .mixed_precision.hip_fused import fused_attention_layer_tail, fused_layer_tail, layer_norm_qkv
     from .mixed_precision.hip_linear import (
-        layer_norm, mixed_ffn_add_layer_norm, mixed_linear, mixed_linear_add_layer_norm, mixed_linear_residual,
-        mixed_linear_residual_layer_norm,
+        layer_norm, mixed_ffn_add_layer_norm, mixed_linear, mixed_linear_add_layer_norm, mixed_linear_q_scaled,
+        mixed_linear_residual, mixed_linear_residual_layer_norm,
     )
 
     import dataclasses
@@ -240,9 +240,22 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
             }
         else:
             normalized = layer_norm(x, layer.norm1, normalized_dtype=sdt)
-            qkv = mixed_linear(normalized, att.qkv_proj, output_dtype=torch.float16, variant=route.qkv_variant)
-            q, k, v = qkv.view(B, S, 3, att.num_heads, att.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
-            ctx = attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant).view(B, S, D)
+            if dispatch.prescaled_attention_for(route, S):
+                # the route's pair: q scaled by the projection, attention without a scale
+                project = lambda: mixed_linear_q_scaled(  # noqa: E731
+                    normalized, att.qkv_proj, D, att.q_prescale, variant=route.qkv_variant)
+                qkv = project()
+                q, k, v = qkv.view(B, S, 3, att.num_heads, att.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
+                attend = lambda: attention_prescaled(  # noqa: E731
+                    q, k, v, causal=causal, variant=route.attention_variant)
+            else:
+                project = lambda: mixed_linear(  # noqa: E731
+                    normalized, att.qkv_proj, output_dtype=torch.float16, variant=route.qkv_variant)
+                qkv = project()
+                q, k, v = qkv.view(B, S, 3, att.num_heads, att.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
+                attend = lambda: attention(  # noqa: E731
+                    q, k, v, att.scale, causal=causal, variant=route.attention_variant)
+            ctx = attend().view(B, S, D)
             if route.wide_ln_epilogue:
                 resid, nffn = mixed_linear_residual_layer_norm(ctx, att.out_proj, x, layer.norm2,
                                                                normalized_dtype=sdt)
@@ -256,9 +269,8 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
                                   variant=route.ffn_in_variant)
             launches = {
                 "layernorm": lambda: layer_norm(x, layer.norm1, normalized_dtype=sdt),
-                "qkv_proj": lambda: mixed_linear(normalized, att.qkv_proj, output_dtype=torch.float16,
-                                                 variant=route.qkv_variant),
-                "attention": lambda: attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant),
+                "qkv_proj": project,
+                "attention": attend,
                 "out_proj_ln": (
                     (lambda: mixed_linear_residual_layer_norm(ctx, att.out_proj, x, layer.norm2, normalized_dtype=sdt))
                     if route.wide_ln_epilogue else
@@ -634,7 +646,7 @@ python bench.py --config cfgN --json-out gpurun_out/bench_cfgN.json
 cd /tmp && export TMPDIR=/tmp && rocprofv3 --kernel-trace --stats --output-format csv \\
     -d $GRAFT_REPO_ROOT/gpurun_out/prof_cfgN -o run -- \\
     python3 $GRAFT_REPO_ROOT/bench.py --config cfgN --no-cpu-baseline --steps 20 --warmup 3
-# on the GPU box, counter passes for N = 2, 4, 5 (one rocprofv3 run per pass; eager forward of
+# on the GPU box, counter passes for N = 1..5 (one rocprofv3 run per pass; eager forward of
 # one microbatch, 3 iterations, after a 1 GiB copy that calibrates FETCH_SIZE / WRITE_SIZE)
 cd /tmp && export TMPDIR=/tmp && PYTHONPATH=$GRAFT_REPO_ROOT rocprofv3 --pmc FETCH_SIZE --output-format csv \\
     -d $GRAFT_REPO_ROOT/gpurun_out/pmc_cfgN_FETCH_SIZE -o run -- python3 -m tiktoktechjam2026_amd.profiling run --config cfgN
