@@ -159,7 +159,8 @@ int mpk_attention_auto_variant(int32_t batch, int32_t heads, int32_t seq_len, in
 /*
  * mpk_causal_attention for FP16 q / k / v whose q already holds q * scale * log2(e), rounded to
  * FP16 once by its producer (mpk_linear_qscaled): the 32x32 kernel (head_dim 32 or 64, variant 0
- * or 6-8) with the scores already in log2 units, so no per-score scaling.  out_dtype kF16 or kF32.
+ * or 6-8; variant 0 picks 6 at head_dim 32) with the scores already in log2 units, so no
+ * per-score scaling.  out_dtype kF16 or kF32.
  * Replaces, with the scale moved into the projection: fp16_causal_attention
  * (custom_kernel/triton_attention.py:341-390).
  */
@@ -191,6 +192,21 @@ int mpk_layer_tail(const void* ctx, const float* x, const void* w_o, const void*
                    float* x_out, void* out, int last, int64_t m, int32_t d, int32_t f, float ln2_eps,
                    float next_ln_eps, int variant, void* stream);
 int mpk_layer_tail_supported(int32_t d, int32_t f);
+
+/*
+ * mpk_layer_tail with the next layer's q columns (out[:, 0:d], last == 0) multiplied by
+ * q_scale in FP32 before the FP16 rounding: the next QKV for mpk_causal_attention_prescaled
+ * (q_scale = scale * log2(e)).  k / v columns, x_out and the last layer's output are those of
+ * mpk_layer_tail bit for bit.
+ * Replaces, with the scale moved into the projection: the calls mpk_layer_tail replaces
+ * (mixed_precision/transformer.py:196-222, :540-560, :88-120); no single reference function
+ * corresponds to it.
+ */
+int mpk_layer_tail_qscaled(const void* ctx, const float* x, const void* w_o, const void* b_o, const float* ln2_w,
+                           const float* ln2_b, const void* w_in, const void* b_in, const void* w_out,
+                           const void* b_out, const float* next_ln_w, const float* next_ln_b, const void* w_qkv,
+                           const void* b_qkv, float* x_out, void* out, int last, int64_t m, int32_t d, int32_t f,
+                           float ln2_eps, float next_ln_eps, float q_scale, int variant, void* stream);
 
 /*
  * Attention + layer tail in one kernel, for head dim 32 (or 16 at d 32 and 64): the causal
@@ -231,6 +247,17 @@ int32_t mpk_attention_layer_tail_rows(void);
 int mpk_layernorm_qkv(const float* x, const float* ln_w, const float* ln_b, const void* w_qkv,
                       const void* b_qkv, void* qkv, int64_t m, int32_t d, float eps, int variant, void* stream);
 int mpk_layernorm_qkv_supported(int32_t d);
+
+/*
+ * mpk_layernorm_qkv with the q columns (qkv[:, 0:d]) multiplied by q_scale in FP32 before the
+ * FP16 rounding (k / v columns bit for bit those of mpk_layernorm_qkv): the first layer's QKV
+ * for mpk_causal_attention_prescaled.
+ * Replaces, with the scale moved into the projection: the initial norm1 + cast
+ * (mixed_precision/transformer.py:484-486) and the first QKV mixed_linear (:88-120).
+ */
+int mpk_layernorm_qkv_qscaled(const float* x, const float* ln_w, const float* ln_b, const void* w_qkv,
+                              const void* b_qkv, void* qkv, int64_t m, int32_t d, float eps, float q_scale,
+                              int variant, void* stream);
 
 #ifdef __cplusplus
 }

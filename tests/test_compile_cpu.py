@@ -29,6 +29,10 @@ ROUTES = {
                               {"mpk.layer_norm.default": 1, "mpk.attention.default": 2}),
     "gemm_d512": (TransformerConfig(2, 64, 512, 8, 2048, 2, True), {"mpk.attention.default": 2}),
     # head dim 32 from 256 positions: q leaves the projection pre-scaled, the attention skips the scale
+    # d_model 128, head dim 32, 256 positions: the layer-tail route's QKV producers scale q
+    "layer_tail_prescaled_d128": (TransformerConfig(1, 256, 128, 4, 128, 2, True),
+                                  {"mpk.layer_norm_qkv.default": 1, "mpk.attention_prescaled.default": 2,
+                                   "mpk.attention.default": 0, "mpk.layer_tail.default": 2}),
     "gemm_prescaled_d256": (TransformerConfig(1, 256, 256, 8, 1024, 2, True),
                             {"mpk.linear_qscaled.default": 2, "mpk.attention_prescaled.default": 2,
                              "mpk.attention.default": 0}),

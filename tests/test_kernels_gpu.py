@@ -684,6 +684,71 @@ def _check_layer_tail(hip_device, d, f, m, last, variant):
 
 
 
+def _check_q_scaled(scaled, plain, d, c, what):
+    """q columns [0, d) of a q-scaled QKV against the unscaled launch's times c: both are one FP16
+    rounding of the same FP32 value (times c), so they differ by at most about one FP16 ulp of
+    the result; k / v columns bit for bit."""
+    assert scaled.dtype == plain.dtype == torch.float16 and scaled.shape == plain.shape
+    assert torch.equal(scaled[..., d:], plain[..., d:]), what
+    q_s = scaled[..., :d].cpu().double()
+    q_u = plain[..., :d].cpu().double() * c
+    err = (q_s - q_u).abs()
+    bound = 2.0 ** -10 * q_u.abs() + 2.0 ** -24  # one ulp at the result's binade, FP16 subnormals
+    assert bool((err <= bound).all()), f"{what}: max err {float(err.max()):.3g}"
+    assert not torch.equal(scaled[..., :d], plain[..., :d]), f"{what}: q left unscaled"
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("m", [5, 9000])
+@pytest.mark.parametrize("variant", [0, 1, 3])
+def test_layer_norm_qkv_q_scaled(hip_device, d, m, variant):
+    """mpk_layernorm_qkv_qscaled: the q columns scaled in FP32 before the FP16 rounding, k / v
+    columns those of mpk_layernorm_qkv bit for bit."""
+    from tiktoktechjam2026_amd.mixed_precision.hip_fused import layer_norm_qkv
+
+    x = _randn((m, d), 51, 2.0).to(hip_device)
+    norm = _norm(d, hip_device, 52)
+    lin = _linear(d, 3 * d, hip_device, 53)
+    c = 0.25503486
+    plain = layer_norm_qkv(x, norm, lin, variant=variant)
+    scaled = layer_norm_qkv(x, norm, lin, variant=variant, q_scale=c)
+    _check_q_scaled(scaled, plain, d, c, "layer_norm_qkv q_scale")
+
+
+@pytest.mark.parametrize("d,f", [(128, 128), (32, 64), (64, 256)])
+@pytest.mark.parametrize("m", [7, 2 * 256 * 128 + 37])
+@pytest.mark.parametrize("variant", [0, 1, 3])
+def test_fused_layer_tail_q_scaled(hip_device, d, f, m, variant):
+    """mpk_layer_tail_qscaled: residual output and k / v columns of the next QKV equal
+    mpk_layer_tail's bit for bit, the q columns are scaled before the FP16 rounding; the last
+    layer ignores the factor."""
+    from tiktoktechjam2026_amd.mixed_precision.hip_fused import fused_layer_tail
+
+    ctx = _randn((m, d), 61).to(hip_device, torch.float16)
+    x = _randn((m, d), 62, 2.0).to(hip_device)
+    mods = [_linear(d, d, hip_device, 63), _norm(d, hip_device, 66), _linear(d, f, hip_device, 64),
+            _linear(f, d, hip_device, 65), _norm(d, hip_device, 67)]
+    qkv_proj = _linear(d, 3 * d, hip_device, 68)
+    c = 0.17677669 * 1.4426950
+    x_p, qkv_p = fused_layer_tail(ctx, x, *mods, qkv_proj, variant=variant)
+    x_s, qkv_s = fused_layer_tail(ctx, x, *mods, qkv_proj, variant=variant, q_scale=c)
+    assert torch.equal(x_p, x_s)
+    _check_q_scaled(qkv_s, qkv_p, d, c, "layer tail q_scale")
+    x_l, n_l = fused_layer_tail(ctx, x, *mods, None, variant=variant)
+    x_ls, n_ls = fused_layer_tail(ctx, x, *mods, None, variant=variant, q_scale=c)
+    assert torch.equal(x_l, x_ls) and torch.equal(n_l, n_ls)
+
+
+def test_q_scale_rejects(hip_device):
+    from tiktoktechjam2026_amd.mixed_precision.hip_fused import layer_norm_qkv
+
+    x = _randn((4, 32), 51).to(hip_device)
+    with pytest.raises(ValueError):
+        layer_norm_qkv(x, _norm(32, hip_device, 52), _linear(32, 96, hip_device, 53), q_scale=float("nan"))
+    with pytest.raises(ValueError):
+        layer_norm_qkv(x, _norm(32, hip_device, 52), _linear(32, 96, hip_device, 53), q_scale=0.0)
+
+
 # --------------------------------------------------------------------------- attention inside the layer tail
 
 

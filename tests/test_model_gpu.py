@@ -124,10 +124,12 @@ PADDED_CASES = [
     TransformerConfig(3, 160, 256, 8, 512, 2, True),  # GEMM route, LayerNorm in the residual GEMMs
     TransformerConfig(2, 130, 512, 8, 1024, 2, True),  # GEMM route, d_model 512
     TransformerConfig(3, 100, 256, 4, 256, 2, False),  # non-causal: valid queries see every valid key
+    TransformerConfig(2, 300, 128, 4, 128, 2, True),   # layer-tail route, q pre-scaled (head dim 32, 300 keys)
+    TransformerConfig(2, 272, 256, 8, 512, 2, True),   # GEMM route, q pre-scaled
 ]
 
 
-@pytest.mark.parametrize("config", PADDED_CASES, ids=[f"d{c.d_model}{'' if c.causal else '_noncausal'}"
+@pytest.mark.parametrize("config", PADDED_CASES, ids=[f"d{c.d_model}s{c.seq_len}{'' if c.causal else '_noncausal'}"
                                                       for c in PADDED_CASES])
 def test_padded_input_matches_oracle(hip_device, config):
     print(f"\n[padded] config={config}", flush=True)
@@ -267,27 +269,36 @@ def test_attention_in_layer_tail_route_is_bit_identical(hip_device, causal, d, h
 
 @pytest.mark.parametrize(
     "d,heads,s,f,prescaled",
-    [(256, 8, 256, 512, True), (256, 8, 128, 512, False), (512, 8, 256, 1024, False), (128, 4, 256, 128, False)],
+    [(256, 8, 256, 512, True), (256, 8, 128, 512, False), (512, 8, 256, 1024, False), (128, 4, 256, 128, True),
+     (128, 4, 128, 128, False)],
 )
 def test_kernel_table_times_the_route_kernels(hip_device, monkeypatch, d, heads, s, f, prescaled):
     """bench.py's per-kernel table (profiling.forward_kernel_table) launches the kernels the
-    forward runs: the pre-scaled projection + attention pair where the route takes it (head dim
-    32 from 256 keys with a separate QKV launch), the scaled ones elsewhere; one row per kernel
-    the forward prices, each with a positive time."""
+    forward runs: where the route pre-scales q (head dim 32 from 256 keys, attention in its own
+    launch) the q-scaling producers (projection, or LayerNorm + QKV and layer tail) and the
+    pre-scaled attention, elsewhere the scaled ones; one row per kernel the forward prices,
+    each with a positive time."""
     from tiktoktechjam2026_amd import dispatch, profiling
     from tiktoktechjam2026_amd.custom_kernel import hip_attention
-    from tiktoktechjam2026_amd.mixed_precision import hip_linear
+    from tiktoktechjam2026_amd.mixed_precision import hip_fused, hip_linear
 
-    calls = {"attention": 0, "attention_prescaled": 0, "mixed_linear_q_scaled": 0}
-    for mod, name in ((hip_attention, "attention"), (hip_attention, "attention_prescaled"),
-                      (hip_linear, "mixed_linear_q_scaled")):
+    calls = {"attention": 0, "attention_prescaled": 0, "q_scaled_producer": 0}
+
+    def count(mod, name, key, only_with_q_scale=False):
         real = getattr(mod, name)
 
-        def counted(*args, _real=real, _name=name, **kwargs):
-            calls[_name] += 1
-            return _real(*args, **kwargs)
+        def counted(*args, **kwargs):
+            if not only_with_q_scale or kwargs.get("q_scale") is not None:
+                calls[key] += 1
+            return real(*args, **kwargs)
 
         monkeypatch.setattr(mod, name, counted)
+
+    count(hip_attention, "attention", "attention")
+    count(hip_attention, "attention_prescaled", "attention_prescaled")
+    count(hip_linear, "mixed_linear_q_scaled", "q_scaled_producer")
+    count(hip_fused, "layer_norm_qkv", "q_scaled_producer", only_with_q_scale=True)
+    count(hip_fused, "fused_layer_tail", "q_scaled_producer", only_with_q_scale=True)
     config = TransformerConfig(2, s, d, heads, f, 2, True)
     _, model = _build(config, hip_device)
     assert dispatch.prescaled_attention_for(model.route, s) == prescaled
@@ -298,6 +309,6 @@ def test_kernel_table_times_the_route_kernels(hip_device, monkeypatch, d, heads,
     assert {r["kernel"] for r in rows} == priced
     assert all(r["avg_us"] > 0 for r in rows)
     if prescaled:
-        assert calls["attention_prescaled"] > 0 and calls["mixed_linear_q_scaled"] > 0 and calls["attention"] == 0
+        assert calls["attention_prescaled"] > 0 and calls["q_scaled_producer"] > 0 and calls["attention"] == 0, calls
     else:
-        assert calls["attention_prescaled"] == 0 and calls["mixed_linear_q_scaled"] == 0
+        assert calls["attention_prescaled"] == 0 and calls["q_scaled_producer"] == 0, calls

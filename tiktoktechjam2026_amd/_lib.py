@@ -103,6 +103,14 @@ SIGNATURES = {
         ],
     ),
     "mpk_layer_tail_supported": (_c_int, [_c_i32, _c_i32]),
+    "mpk_layer_tail_qscaled": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i32,
+            _c_i32, _c_float, _c_float, _c_float, _c_int, _c_void_p,
+        ],
+    ),
     "mpk_attention_layer_tail": (
         _c_int,
         [
@@ -118,6 +126,11 @@ SIGNATURES = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i32, _c_float, _c_int, _c_void_p],
     ),
     "mpk_layernorm_qkv_supported": (_c_int, [_c_i32]),
+    "mpk_layernorm_qkv_qscaled": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i32, _c_float, _c_float, _c_int,
+         _c_void_p],
+    ),
 }
 
 _lock = threading.Lock()

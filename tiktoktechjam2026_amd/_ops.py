@@ -385,37 +385,41 @@ def _(q, k, v, key_valid, causal, out_dtype, variant):
 @torch.library.custom_op("mpk::layer_norm_qkv", mutates_args=())
 def layer_norm_qkv(
     x: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor, w_qkv: torch.Tensor, b_qkv: torch.Tensor, eps: float,
-    variant: int,
+    variant: int, q_scale: float = 0.0,
 ) -> torch.Tensor:
-    """``fp16(LayerNorm(x)) W_qkv^T + b`` -> FP16 ``[..., 3D]`` (``mpk_layernorm_qkv``)."""
+    """``fp16(LayerNorm(x)) W_qkv^T + b`` -> FP16 ``[..., 3D]`` (``mpk_layernorm_qkv``); with
+    ``q_scale`` != 0 the q columns are multiplied by it before the FP16 rounding
+    (``mpk_layernorm_qkv_qscaled``)."""
     d = x.shape[-1]
     out = torch.empty((*x.shape[:-1], 3 * d), device=x.device, dtype=torch.float16)
     _require_aligned("unsupported LayerNorm/QKV inputs", x, ln_w, ln_b, w_qkv, b_qkv, out)
-    _lib.check(
-        _lib.load().mpk_layernorm_qkv(
-            x.data_ptr(), ln_w.data_ptr(), ln_b.data_ptr(), w_qkv.data_ptr(), b_qkv.data_ptr(), out.data_ptr(),
-            _rows(x, d), d, float(eps), int(variant), _lib.stream_handle(x.device),
-        ),
-        "mpk_layernorm_qkv",
-    )
+    lib = _lib.load()
+    args = (x.data_ptr(), ln_w.data_ptr(), ln_b.data_ptr(), w_qkv.data_ptr(), b_qkv.data_ptr(), out.data_ptr(),
+            _rows(x, d), d, float(eps))
+    tail = (int(variant), _lib.stream_handle(x.device))
+    if q_scale:
+        _lib.check(lib.mpk_layernorm_qkv_qscaled(*args, float(q_scale), *tail), "mpk_layernorm_qkv_qscaled")
+    else:
+        _lib.check(lib.mpk_layernorm_qkv(*args, *tail), "mpk_layernorm_qkv")
     return out
 
 
 @layer_norm_qkv.register_fake
-def _(x, ln_w, ln_b, w_qkv, b_qkv, eps, variant):
+def _(x, ln_w, ln_b, w_qkv, b_qkv, eps, variant, q_scale=0.0):
     return x.new_empty((*x.shape[:-1], 3 * x.shape[-1]), dtype=torch.float16)
 
 
 @torch.library.custom_op("mpk::layer_tail", mutates_args=())
 def layer_tail(
     ctx: torch.Tensor, residual: torch.Tensor, tensors: List[torch.Tensor], w_qkv: Optional[torch.Tensor],
-    b_qkv: Optional[torch.Tensor], ln2_eps: float, next_eps: float, variant: int,
+    b_qkv: Optional[torch.Tensor], ln2_eps: float, next_eps: float, variant: int, q_scale: float = 0.0,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Out-projection through the next layer's QKV (or the final LayerNorm) in one kernel (``mpk_layer_tail``).
 
     ``tensors`` = [w_o, b_o, ln2_w, ln2_b, w_in, b_in, w_out, b_out, next_ln_w, next_ln_b].
     Returns ``(residual_out, qkv FP16 [..., 3D])``, or ``(residual_out, normalized FP32)``
-    when ``w_qkv`` is None (last layer).
+    when ``w_qkv`` is None (last layer).  ``q_scale`` != 0 multiplies the next q columns by it
+    before the FP16 rounding (``mpk_layer_tail_qscaled``).
     """
     w_o, b_o, ln2_w, ln2_b, w_in, b_in, w_out, b_out, next_w, next_b = tensors
     d = ctx.shape[-1]
@@ -425,20 +429,21 @@ def layer_tail(
     shape = ctx.shape if last else (*ctx.shape[:-1], 3 * d)
     out = torch.empty(shape, device=ctx.device, dtype=torch.float32 if last else torch.float16)
     _require_aligned("unsupported fused layer-tail inputs", ctx, residual, *tensors, w_qkv, b_qkv, residual_out, out)
-    _lib.check(
-        _lib.load().mpk_layer_tail(
-            ctx.data_ptr(), residual.data_ptr(), w_o.data_ptr(), b_o.data_ptr(), ln2_w.data_ptr(), ln2_b.data_ptr(),
+    lib = _lib.load()
+    args = (ctx.data_ptr(), residual.data_ptr(), w_o.data_ptr(), b_o.data_ptr(), ln2_w.data_ptr(), ln2_b.data_ptr(),
             w_in.data_ptr(), b_in.data_ptr(), w_out.data_ptr(), b_out.data_ptr(), next_w.data_ptr(),
             next_b.data_ptr(), _ptr(w_qkv), _ptr(b_qkv), residual_out.data_ptr(), out.data_ptr(), 1 if last else 0,
-            _rows(ctx, d), d, f, float(ln2_eps), float(next_eps), int(variant), _lib.stream_handle(ctx.device),
-        ),
-        "mpk_layer_tail",
-    )
+            _rows(ctx, d), d, f, float(ln2_eps), float(next_eps))
+    tail = (int(variant), _lib.stream_handle(ctx.device))
+    if q_scale:
+        _lib.check(lib.mpk_layer_tail_qscaled(*args, float(q_scale), *tail), "mpk_layer_tail_qscaled")
+    else:
+        _lib.check(lib.mpk_layer_tail(*args, *tail), "mpk_layer_tail")
     return residual_out, out
 
 
 @layer_tail.register_fake
-def _(ctx, residual, tensors, w_qkv, b_qkv, ln2_eps, next_eps, variant):
+def _(ctx, residual, tensors, w_qkv, b_qkv, ln2_eps, next_eps, variant, q_scale=0.0):
     d = ctx.shape[-1]
     if w_qkv is None:
         return torch.empty_like(residual), ctx.new_empty(ctx.shape, dtype=torch.float32)

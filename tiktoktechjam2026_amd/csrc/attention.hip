@@ -1316,7 +1316,11 @@ extern "C" int mpk_causal_attention_prescaled(const void* q, const void* k, cons
   if (batch < 0 || heads <= 0 || seq_len < 0) return MPK_EINVAL;
   if (out_dtype != kF32 && out_dtype != kF16) return MPK_EINVAL;
   if (head_dim != 32 && head_dim != 64) return MPK_EUNSUPPORTED;
-  if (variant == 0) variant = head_dim == 32 ? (seq_len >= 4096 ? 7 : 6) : (seq_len < 1024 ? 7 : 6);
+  // built-in choice: 4-wave workgroups at head dim 32 (without the per-score FMA they are at
+  // least as fast as the 8-wave ones at every length measured on MI355X: 764 vs 783 us alone
+  // at B64 H8 S4096, level within 0.2 % in the whole cfg5 forward), as
+  // mpk_attention_auto_variant at head dim 64
+  if (variant == 0) variant = head_dim == 32 ? 6 : (seq_len < 1024 ? 7 : 6);
   if (variant < 6 || variant > 8) return MPK_EUNSUPPORTED;
   const int64_t* st[4] = {q_strides, k_strides, v_strides, o_strides};
   const void* base[4] = {q, k, v, o};

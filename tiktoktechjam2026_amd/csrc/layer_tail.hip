@@ -59,6 +59,10 @@ struct TailArgs {
   const _Float16* qkv_in;
   int seq, causal;
   float attn_c;
+  // the next QKV's q columns [0, D) multiplied by q_scale in FP32 before the FP16 rounding
+  // (q_on != 0: mpk_layer_tail_qscaled / mpk_layernorm_qkv_qscaled, for the pre-scaled attention)
+  int q_on;
+  float q_scale;
 };
 
 constexpr int kLdsBudget = 160 * 1024;
@@ -940,6 +944,7 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
         const int n = 32 * op + 8 * g;
         float bv[8];
         lds8(prm + SH::P_BQKV + n, bv);
+        const bool qcols = a.q_on && 32 * op < D;  // a 32-column block is all q or none (D % 32 == 0)
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
           float v[8];
@@ -947,6 +952,11 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
           for (int i = 0; i < 4; ++i) {
             v[i] = qacc[t][0][i] + bv[i];
             v[4 + i] = qacc[t][1][i] + bv[4 + i];
+          }
+          if (qcols) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] *= a.q_scale;
+            pin_f32x8(v);  // rounded to FP32 first, then to FP16 by the store
           }
           buffer_store8(qres, (uint32_t)((16 * t + r) * (3 * D) + n) * 2u, v, qkv);
         }
@@ -989,6 +999,11 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
           float o[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) o[i] = acc[nt][i] + bq[nt][i];
+          if (a.q_on && ncol0 + 16 * nt < D) {  // wave-uniform: a 16-column tile is all q or none
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] *= a.q_scale;
+            pin_f32x4(o);  // rounded to FP32 first, then to FP16 by the store
+          }
           buffer_store4(qres, (uint32_t)((16 * mt + r) * (3 * D) + ncol0 + 16 * nt + 4 * g) * 2u, o);
         }
       }
@@ -1106,11 +1121,11 @@ extern "C" int mpk_layer_tail_supported(int32_t d, int32_t f) {
          (d == 128 && f == 128) || (d == 32 && f == 32) || (d == 32 && f == 128);
 }
 
-extern "C" int mpk_layer_tail(const void* ctx, const float* x, const void* w_o, const void* b_o, const float* ln2_w,
-                              const float* ln2_b, const void* w_in, const void* b_in, const void* w_out,
-                              const void* b_out, const float* next_ln_w, const float* next_ln_b, const void* w_qkv,
-                              const void* b_qkv, float* x_out, void* out, int last, int64_t m, int32_t d, int32_t f,
-                              float ln2_eps, float next_ln_eps, int variant, void* stream) {
+static int layer_tail_entry(const void* ctx, const float* x, const void* w_o, const void* b_o, const float* ln2_w,
+                            const float* ln2_b, const void* w_in, const void* b_in, const void* w_out,
+                            const void* b_out, const float* next_ln_w, const float* next_ln_b, const void* w_qkv,
+                            const void* b_qkv, float* x_out, void* out, int last, int64_t m, int32_t d, int32_t f,
+                            float ln2_eps, float next_ln_eps, bool q_on, float q_scale, int variant, void* stream) {
   if (!ctx || !x || !w_o || !b_o || !ln2_w || !ln2_b || !w_in || !b_in || !w_out || !b_out || !next_ln_w ||
       !next_ln_b || !x_out || !out || m < 0)
     return MPK_EINVAL;
@@ -1131,6 +1146,7 @@ extern "C" int mpk_layer_tail(const void* ctx, const float* x, const void* w_o, 
   a.g1 = next_ln_w; a.be1 = next_ln_b;
   a.wqkv = static_cast<const _Float16*>(w_qkv); a.bqkv = static_cast<const _Float16*>(b_qkv);
   a.x_out = x_out; a.out = out; a.m = m; a.f = f; a.eps2 = ln2_eps; a.eps1 = next_ln_eps;
+  a.q_on = q_on && !last; a.q_scale = q_scale;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool L = last != 0;
   hipError_t e;
@@ -1142,6 +1158,25 @@ extern "C" int mpk_layer_tail(const void* ctx, const float* x, const void* w_o, 
   else if (d == 64 && f == 256) e = tail_variant<64, 256, true>(variant, L, a, s);
   else e = tail_variant<128, 128, true>(variant, L, a, s);
   return (int)e;
+}
+
+extern "C" int mpk_layer_tail(const void* ctx, const float* x, const void* w_o, const void* b_o, const float* ln2_w,
+                              const float* ln2_b, const void* w_in, const void* b_in, const void* w_out,
+                              const void* b_out, const float* next_ln_w, const float* next_ln_b, const void* w_qkv,
+                              const void* b_qkv, float* x_out, void* out, int last, int64_t m, int32_t d, int32_t f,
+                              float ln2_eps, float next_ln_eps, int variant, void* stream) {
+  return layer_tail_entry(ctx, x, w_o, b_o, ln2_w, ln2_b, w_in, b_in, w_out, b_out, next_ln_w, next_ln_b, w_qkv,
+                          b_qkv, x_out, out, last, m, d, f, ln2_eps, next_ln_eps, false, 1.0f, variant, stream);
+}
+
+extern "C" int mpk_layer_tail_qscaled(const void* ctx, const float* x, const void* w_o, const void* b_o,
+                                      const float* ln2_w, const float* ln2_b, const void* w_in, const void* b_in,
+                                      const void* w_out, const void* b_out, const float* next_ln_w,
+                                      const float* next_ln_b, const void* w_qkv, const void* b_qkv, float* x_out,
+                                      void* out, int last, int64_t m, int32_t d, int32_t f, float ln2_eps,
+                                      float next_ln_eps, float q_scale, int variant, void* stream) {
+  return layer_tail_entry(ctx, x, w_o, b_o, ln2_w, ln2_b, w_in, b_in, w_out, b_out, next_ln_w, next_ln_b, w_qkv,
+                          b_qkv, x_out, out, last, m, d, f, ln2_eps, next_ln_eps, true, q_scale, variant, stream);
 }
 
 extern "C" int mpk_attention_layer_tail_supported(int32_t d, int32_t f, int32_t heads) {
@@ -1210,9 +1245,9 @@ extern "C" int mpk_attention_layer_tail(const void* qkv_in, const float* x, cons
 
 extern "C" int mpk_layernorm_qkv_supported(int32_t d) { return d == 32 || d == 64 || d == 128; }
 
-extern "C" int mpk_layernorm_qkv(const float* x, const float* ln_w, const float* ln_b, const void* w_qkv,
-                                 const void* b_qkv, void* qkv, int64_t m, int32_t d, float eps, int variant,
-                                 void* stream) {
+static int layernorm_qkv_entry(const float* x, const float* ln_w, const float* ln_b, const void* w_qkv,
+                               const void* b_qkv, void* qkv, int64_t m, int32_t d, float eps, bool q_on,
+                               float q_scale, int variant, void* stream) {
   if (!x || !ln_w || !ln_b || !w_qkv || !b_qkv || !qkv || m < 0) return MPK_EINVAL;
   if (!mpk_layernorm_qkv_supported(d)) return MPK_EUNSUPPORTED;
   const void* ptrs[] = {x, ln_w, ln_b, w_qkv, b_qkv, qkv};
@@ -1225,6 +1260,7 @@ extern "C" int mpk_layernorm_qkv(const float* x, const float* ln_w, const float*
   a.x = x; a.g1 = ln_w; a.be1 = ln_b;
   a.wqkv = static_cast<const _Float16*>(w_qkv); a.bqkv = static_cast<const _Float16*>(b_qkv);
   a.out = qkv; a.m = m; a.eps1 = eps;
+  a.q_on = q_on; a.q_scale = q_scale;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   switch (d) {
@@ -1233,4 +1269,16 @@ extern "C" int mpk_layernorm_qkv(const float* x, const float* ln_w, const float*
     default: e = tail_variant<128, 32, false>(variant, false, a, s); break;
   }
   return (int)e;
+}
+
+extern "C" int mpk_layernorm_qkv(const float* x, const float* ln_w, const float* ln_b, const void* w_qkv,
+                                 const void* b_qkv, void* qkv, int64_t m, int32_t d, float eps, int variant,
+                                 void* stream) {
+  return layernorm_qkv_entry(x, ln_w, ln_b, w_qkv, b_qkv, qkv, m, d, eps, false, 1.0f, variant, stream);
+}
+
+extern "C" int mpk_layernorm_qkv_qscaled(const float* x, const float* ln_w, const float* ln_b, const void* w_qkv,
+                                         const void* b_qkv, void* qkv, int64_t m, int32_t d, float eps,
+                                         float q_scale, int variant, void* stream) {
+  return layernorm_qkv_entry(x, ln_w, ln_b, w_qkv, b_qkv, qkv, m, d, eps, true, q_scale, variant, stream);
 }

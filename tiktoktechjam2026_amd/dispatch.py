@@ -130,8 +130,9 @@ class Route:
     fuse_layer_tail: bool = False
     fuse_attention_tail: bool = False  # attention inside the layer tail, up to attention_tail_max_seq positions
     attention_tail_max_seq: int = 0
-    # head dim 32 off the layer-tail route: from 256 keys the QKV projection folds the attention
-    # scale into q and the 32x32 attention kernel skips its per-score FMA (prescaled_attention_for)
+    # head dim 32: from 256 keys the QKV producer (projection, layer tail or LayerNorm + QKV)
+    # folds the attention scale into q and the 32x32 attention kernel skips its per-score FMA
+    # (prescaled_attention_for; not where attention runs inside the layer tail)
     prescale_q: bool = False
     wide_ln_epilogue: bool = False
     wide_ln_ffn_out: bool = False
@@ -221,7 +222,7 @@ def plan(
         fuse_layer_tail=fuse_tail,
         fuse_attention_tail=fuse_attn_tail,
         attention_tail_max_seq=attn_tail_max_seq,
-        prescale_q=enable_fp16_custom_attention and not fuse_tail and hd == 32,
+        prescale_q=enable_fp16_custom_attention and hd == 32,
         wide_ln_epilogue=wide_ln,
         wide_ln_ffn_out=wide_ln and d in WIDE_LN_FFN_OUT_WIDTHS,
     )
@@ -246,8 +247,10 @@ PRESCALED_ATTENTION_MIN_SEQ = 256
 
 def prescaled_attention_for(route: Route, seq_len: int) -> bool:
     """Whether a forward over ``seq_len`` positions projects q pre-multiplied by the attention's
-    scale * log2(e) and runs ``attention_prescaled`` (measured on MI355X: cfg5's attention
-    -6 %, 810 vs 862 us, from the per-score FMA it no longer needs; cfg2's -2 %)."""
+    scale * log2(e) and runs ``attention_prescaled`` as a launch of its own (the layer-tail route
+    checks ``attention_tail_for`` first: attention inside the tail keeps its scaling).  Measured
+    on MI355X in one process: attention at cfg5's shape 831 -> 764 us, at cfg2's 36 -> 34 us,
+    from the per-score FMA it no longer needs."""
     return (
         route.prescale_q and seq_len >= PRESCALED_ATTENTION_MIN_SEQ and route.attention_variant in (0, 6, 7, 8)
     )

@@ -17,6 +17,7 @@ launches on torch's current stream.
 
 from __future__ import annotations
 
+import math
 from typing import Optional, Tuple
 
 import torch
@@ -37,8 +38,13 @@ def layer_norm_qkv_supported(d_model: int) -> bool:
     return int(d_model) in LAYERNORM_QKV_WIDTHS
 
 
-def layer_norm_qkv(x: torch.Tensor, norm: nn.LayerNorm, qkv_proj: nn.Linear, *, variant: int = 0) -> torch.Tensor:
-    """``fp16(LayerNorm(x)) @ Wqkv^T + b`` -> FP16 ``[..., 3D]`` (FP32 statistics and accumulation)."""
+def layer_norm_qkv(
+    x: torch.Tensor, norm: nn.LayerNorm, qkv_proj: nn.Linear, *, variant: int = 0, q_scale: Optional[float] = None
+) -> torch.Tensor:
+    """``fp16(LayerNorm(x)) @ Wqkv^T + b`` -> FP16 ``[..., 3D]`` (FP32 statistics and accumulation).
+
+    ``q_scale``: the q columns leave multiplied by it (in FP32, before the FP16 rounding), the
+    input ``attention_prescaled`` takes with ``q_scale = scale * log2(e)``."""
     d = x.shape[-1] if x.dim() else 0
     if not (
         _gpu(x)
@@ -51,7 +57,17 @@ def layer_norm_qkv(x: torch.Tensor, norm: nn.LayerNorm, qkv_proj: nn.Linear, *, 
     ):
         raise ValueError("unsupported LayerNorm/QKV inputs")
     return _ops.layer_norm_qkv(x, norm.weight, norm.bias, qkv_proj.weight, qkv_proj.bias, float(norm.eps),
-                               int(variant))
+                               int(variant), _q_scale(q_scale))
+
+
+def _q_scale(q_scale: Optional[float]) -> float:
+    """The custom ops' encoding: 0.0 for no q scaling, else a finite nonzero FP32 factor."""
+    if q_scale is None:
+        return 0.0
+    q = float(q_scale)
+    if not math.isfinite(q) or q == 0.0:
+        raise ValueError("q_scale must be finite and nonzero")
+    return q
 
 
 def fused_layer_tail(
@@ -65,12 +81,14 @@ def fused_layer_tail(
     next_qkv_proj: Optional[nn.Linear] = None,
     *,
     variant: int = 0,
+    q_scale: Optional[float] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Attention output projection through the next layer's QKV projection in one kernel.
 
     Returns ``(residual_out, qkv)`` with ``qkv`` FP16 ``[..., 3D]``, or, when
     ``next_qkv_proj`` is None (last layer), ``(residual_out, normalized)`` with
-    ``normalized = next_norm(residual_out)`` in FP32.
+    ``normalized = next_norm(residual_out)`` in FP32.  ``q_scale`` as for ``layer_norm_qkv``
+    (ignored for the last layer, which has no next QKV).
     """
     d = ctx.shape[-1] if ctx.dim() else 0
     f = ffn_in.out_features
@@ -97,7 +115,7 @@ def fused_layer_tail(
                ffn_out.weight, ffn_out.bias, next_norm.weight, next_norm.bias]
     return _ops.layer_tail(
         ctx, residual, tensors, None if last else next_qkv_proj.weight, None if last else next_qkv_proj.bias,
-        float(norm2.eps), float(next_norm.eps), int(variant),
+        float(norm2.eps), float(next_norm.eps), int(variant), 0.0 if last else _q_scale(q_scale),
     )
 
 

@@ -102,11 +102,18 @@ class MixedPrecisionSelfAttention(nn.Module):
         qkv = mixed_linear(normalized, self.qkv_proj, output_dtype=qkv_dtype, variant=route.qkv_variant)
         return self.attend(qkv, key_valid, causal)
 
-    def attend(self, qkv: torch.Tensor, key_valid: Optional[torch.Tensor], causal: bool) -> torch.Tensor:
-        """Flash attention over a packed ``[B, S, 3D]`` projection -> context ``[B, S, D]``."""
+    def attend(
+        self, qkv: torch.Tensor, key_valid: Optional[torch.Tensor], causal: bool, prescaled: bool = False
+    ) -> torch.Tensor:
+        """Flash attention over a packed ``[B, S, 3D]`` projection -> context ``[B, S, D]``;
+        ``prescaled``: q already holds q * scale * log2(e) (FP16), for ``attention_prescaled``."""
         batch, seq_len, _ = qkv.shape
         q, k, v = qkv.view(batch, seq_len, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
-        ctx = attention(q, k, v, self.scale, causal=causal, key_valid=key_valid, variant=self.route.attention_variant)
+        if prescaled:
+            ctx = attention_prescaled(q, k, v, causal=causal, key_valid=key_valid, variant=self.route.attention_variant)
+        else:
+            ctx = attention(q, k, v, self.scale, causal=causal, key_valid=key_valid,
+                            variant=self.route.attention_variant)
         return ctx.view(batch, seq_len, self.d_model)
 
     def forward(
@@ -303,9 +310,9 @@ class MixedPrecisionTransformer(nn.Module):
 def _forward_layer_tail_impl(model: "MixedPrecisionTransformer", x, key_valid, causal):
     route = model.route
     layers = model.layers
-    qkv = layer_norm_qkv(x, layers[0].norm1, layers[0].attention.qkv_proj, variant=route.head_variant)
     if dispatch.attention_tail_for(route, x.shape[1], key_valid is not None):
         # 1 + L launches: each layer's attention runs inside its layer-tail kernel
+        qkv = layer_norm_qkv(x, layers[0].norm1, layers[0].attention.qkv_proj, variant=route.head_variant)
         result = None
         for index, layer in enumerate(layers):
             att = layer.attention
@@ -320,10 +327,19 @@ def _forward_layer_tail_impl(model: "MixedPrecisionTransformer", x, key_valid, c
             else:
                 qkv = out
         return result
+    # two launches per layer; at head dim 32 from 256 keys every QKV producer folds the
+    # attention's scale * log2(e) into q, and the attention kernel skips its per-score FMA
+    prescaled = bool(dispatch.prescaled_attention_for(route, x.shape[1]))
+
+    def q_scale(layer):
+        return layer.attention.q_prescale if prescaled else None
+
+    qkv = layer_norm_qkv(x, layers[0].norm1, layers[0].attention.qkv_proj, variant=route.head_variant,
+                         q_scale=q_scale(layers[0]))
     result = None
     for index, layer in enumerate(layers):
         att = layer.attention
-        ctx = att.attend(qkv, key_valid, causal)
+        ctx = att.attend(qkv, key_valid, causal, prescaled)
         last = index + 1 == len(layers)
         if last:
             x, result = fused_layer_tail(
@@ -334,7 +350,7 @@ def _forward_layer_tail_impl(model: "MixedPrecisionTransformer", x, key_valid, c
             nxt = layers[index + 1]
             x, qkv = fused_layer_tail(
                 ctx, x, att.out_proj, layer.norm2, layer.ffn_in, layer.ffn_out, nxt.norm1, nxt.attention.qkv_proj,
-                variant=route.tail_variant,
+                variant=route.tail_variant, q_scale=q_scale(nxt),
             )
     return result
 

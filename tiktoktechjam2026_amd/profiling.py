@@ -226,14 +226,24 @@ def forward_kernel_table(model, x: torch.Tensor, iterations: int = 50) -> List[D
                     model.final_norm, None),
             }
         elif route.fuse_layer_tail:
-            qkv = layer_norm_qkv(x, layer.norm1, att.qkv_proj, variant=route.head_variant)
+            # the route's QKV producers fold scale * log2(e) into q where the attention takes it
+            qs = att.q_prescale if dispatch.prescaled_attention_for(route, S) else None
+            qkv = layer_norm_qkv(x, layer.norm1, att.qkv_proj, variant=route.head_variant, q_scale=qs)
             q, k, v = qkv.view(B, S, 3, att.num_heads, att.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
-            ctx = attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant).view(B, S, D)
+            if qs is None:
+                attend = lambda: attention(  # noqa: E731
+                    q, k, v, att.scale, causal=causal, variant=route.attention_variant)
+            else:
+                attend = lambda: attention_prescaled(  # noqa: E731
+                    q, k, v, causal=causal, variant=route.attention_variant)
+            ctx = attend().view(B, S, D)
             launches = {
-                "layernorm_qkv": lambda: layer_norm_qkv(x, layer.norm1, att.qkv_proj, variant=route.head_variant),
-                "attention": lambda: attention(q, k, v, att.scale, causal=causal, variant=route.attention_variant),
+                "layernorm_qkv": lambda: layer_norm_qkv(x, layer.norm1, att.qkv_proj, variant=route.head_variant,
+                                                        q_scale=qs),
+                "attention": attend,
                 "layer_tail": lambda: fused_layer_tail(ctx, x, att.out_proj, layer.norm2, layer.ffn_in, layer.ffn_out,
-                                                       layer.norm1, att.qkv_proj, variant=route.tail_variant),
+                                                       layer.norm1, att.qkv_proj, variant=route.tail_variant,
+                                                       q_scale=qs),
                 "layer_tail_last": lambda: fused_layer_tail(ctx, x, att.out_proj, layer.norm2, layer.ffn_in,
                                                             layer.ffn_out, model.final_norm, None,
                                                             variant=route.tail_variant),
