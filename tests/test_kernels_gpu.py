@@ -495,6 +495,37 @@ def test_attention_rising_scores(hip_device, variant, pattern):
         _close(out, _ref_attention(q, k, v, scale, True), 3e-3, 3e-3, f"rising scores ({pattern})")
 
 
+@pytest.mark.parametrize("variant", [6, 7, 8])
+@pytest.mark.parametrize("pattern", ["ramp", "spikes"])
+def test_attention_prescaled_rising_scores(hip_device, variant, pattern):
+    """Pre-scaled q with scores that keep rising: steady head-dim-32 tiles (accumulators started
+    at -m) raise the row max through their exact-max fallback, head dim 64 and 128-key tiles
+    through the ordinary score test with c = 1; weights that would overflow FP16 against a stale
+    max included."""
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention_prescaled
+
+    for b, h, s, hd in ((2, 2, 1024, 32), (1, 2, 600, 64), (1, 2, 2048, 64)):
+        qkv = _randn((b, s, 3, h, hd), 61, 1.0)
+        if pattern == "ramp":
+            qkv[:, :, 1] *= torch.linspace(0.25, 10.0, s)[None, :, None, None]
+        else:
+            for pos, mult in ((130, 6.0), (400, 12.0), (s - 50, 20.0)):
+                qkv[:, pos, 1] *= mult
+        scale = hd ** -0.5
+        c = float(torch.tensor(scale, dtype=torch.float32) * torch.tensor(1.4426950408889634, dtype=torch.float32))
+        qkv_ps = qkv.clone()
+        qkv_ps[:, :, 0] *= c
+        qkv16 = qkv.to(hip_device, torch.float16)
+        q, k, v = qkv16.permute(2, 0, 3, 1, 4).unbind(0)
+        qs = qkv_ps.to(hip_device, torch.float16).permute(2, 0, 3, 1, 4)[0]
+        out = attention_prescaled(qs, k, v, causal=True, variant=variant)
+        assert torch.isfinite(out).all()
+        # the reference takes the kernel's own FP16 q * c, so large scores do not magnify the
+        # difference between rounding q and rounding q * c: softmax(q' k^T ln 2) = 2^(q' k^T)
+        ref = _ref_attention(qs, k, v, 1.0 / 1.4426950408889634, True)
+        _close(out, ref, 3e-3, 3e-3, f"pre-scaled rising scores ({pattern}, hd {hd})")
+
+
 @pytest.mark.parametrize("variant", [6, 7])
 def test_attention_32x32_grouped_schedule(hip_device, variant):
     """A launch with at least 1024 workgroups per XCD walks its (batch, head) rows in groups
