@@ -164,7 +164,7 @@ def test_gelu_epilogue_accuracy(hip_device, n, variant):
         lin.weight.zero_()
         lin.weight[:, 0] = 1.0
         lin.bias.zero_()
-    y = mixed_linear(x.to(hip_device), lin, output_dtype=torch.float32, fuse_gelu=True, variant=variant)
+    y = mixed_linear(x.to(hip_device), lin, output_dtype=torch.float32, fuse_gelu=True, variant=variant).detach()
     vd = v.double()
     ref = 0.5 * vd * (1.0 + torch.erf(vd / math.sqrt(2.0)))
     err = (y.cpu().double() - ref[:, None]).abs()
@@ -524,6 +524,30 @@ def test_attention_prescaled_rising_scores(hip_device, variant, pattern):
         # difference between rounding q and rounding q * c: softmax(q' k^T ln 2) = 2^(q' k^T)
         ref = _ref_attention(qs, k, v, 1.0 / 1.4426950408889634, True)
         _close(out, ref, 3e-3, 3e-3, f"pre-scaled rising scores ({pattern}, hd {hd})")
+
+
+@pytest.mark.parametrize("variant", [6, 7])
+def test_attention_prescaled_wide_row_max(hip_device, variant):
+    """Pre-scaled q whose row maxima grow past the range in which the kernel keeps them as FP16
+    values (|m| >= 2048 in log2 units): keys of the second half 60x larger, so each wave
+    switches from the MFMA-initialised steady tiles to the FP32 splat mid-row; batch row 1
+    keeps ordinary scores.  Against float64 of the kernel's own q."""
+    from tiktoktechjam2026_amd.custom_kernel.hip_attention import attention_prescaled
+
+    b, h, s, hd = 2, 2, 1024, 32
+    qkv = _randn((b, s, 3, h, hd), 71, 1.0)
+    qkv[0, s // 2:, 1] *= 60.0
+    qkv[0, :, 0] *= 15.0
+    qkv16 = qkv.to(hip_device, torch.float16)
+    q, k, v = qkv16.permute(2, 0, 3, 1, 4).unbind(0)
+    c = float(torch.tensor(hd ** -0.5, dtype=torch.float32) * torch.tensor(1.4426950408889634, dtype=torch.float32))
+    qs = (q.float() * c).half()
+    out = attention_prescaled(qs, k, v, causal=True, variant=variant)
+    assert torch.isfinite(out).all()
+    ref = _ref_attention(qs, k, v, 1.0 / 1.4426950408889634, True)
+    top = (qs[0].double().cpu() @ k[0].double().cpu().transpose(-1, -2)).amax()
+    assert float(top) > 4096, float(top)  # the test reaches the wide range
+    _close(out, ref, 3e-3, 3e-3, "pre-scaled attention, row maxima past 2048")
 
 
 @pytest.mark.parametrize("variant", [6, 7])

@@ -774,6 +774,29 @@ void attention32_kernel(AttnArgs a) {
 
   float mrow = 0.f;     // running max of s*c (log2 units) of this lane's query
   bool fresh = true;    // no visible key seen yet
+  // Pre-scaled steady tiles start every S^T block at -m with one 32x32x8 MFMA instead of
+  // VALU moves: A selects k = 0 for every key row (msel), B holds fp16(-m) of the lane's
+  // query at k = 0 (mneg, lanes 0..31), so D[key][query] = -m.  For that the row max is
+  // kept as an FP16 value: rounded to the nearest one when raised (any m works, as long as
+  // acc and l share it; within 0.5 of the true max, weights stay <= 2^0.5) while every
+  // |m| of the wave is below kExactMaxLimit; once one is not (mwide, sticky), the steady
+  // tiles splat the FP32 -m with moves instead.
+  typedef _Float16 h4m __attribute__((ext_vector_type(4)));
+  h4m msel, mneg;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) msel[j] = (_Float16)0.0f, mneg[j] = (_Float16)0.0f;
+  if (hf == 0) msel[0] = (_Float16)1.0f;
+  constexpr float kExactMaxLimit = 2048.f;  // FP16 spacing <= 1 below it
+  int mwide = 0;
+  auto round_m = [&](float m) { return (PS && fabsf(m) < kExactMaxLimit) ? (float)(_Float16)m : m; };
+  // after every update of mrow, in wave-uniform control flow (the ballot needs all lanes)
+  auto set_mneg = [&]() {
+    if constexpr (PS) {
+      if (hf == 0) mneg[0] = (_Float16)(-mrow);
+      mwide = __builtin_amdgcn_readfirstlane(
+          mwide | (__builtin_amdgcn_ballot_w64(!(fabsf(mrow) < kExactMaxLimit)) != 0));
+    }
+  };
   f16v oacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
@@ -878,16 +901,16 @@ void attention32_kernel(AttnArgs a) {
     constexpr bool STEADY = !EDGE && !MAYBE_FRESH && HD == 32 && KTILE == 64;
     const float sc0 = (PS && STEADY) ? -mrow : 0.f;
     f16v sc[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      if (EDGE && nb >= nbv) break;
-      if constexpr (PS && STEADY) {
-        // -m into all 16 accumulator registers on every steady tile: one pair
-        // (-m, -m), then seven 64-bit moves instead of fifteen 32-bit ones (the
-        // compiler splats a scalar with 32-bit moves only; the immediate keeps the
-        // seven statements distinct so they are not merged into one).  The
-        // hazard recognizer counts an asm statement's outputs as VALU writes and
-        // puts the wait states an MFMA source needs after them.
+    f16v cinit;  // pre-scaled steady tiles: -m in every register, the start of each block's S^T
+    if constexpr (PS && STEADY) {
+      if (__builtin_amdgcn_readfirstlane(mwide) == 0) {
+        cinit = __builtin_amdgcn_mfma_f32_32x32x8f16(msel, mneg, f16v{}, 0, 0, 0);
+      } else {
+        // -m splat: one pair (-m, -m), then seven 64-bit moves instead of fifteen 32-bit
+        // ones (the compiler splats a scalar with 32-bit moves only; the immediate keeps
+        // the seven statements distinct so they are not merged into one).  The hazard
+        // recognizer counts an asm statement's outputs as VALU writes and puts the wait
+        // states an MFMA source needs after them.
         typedef float f2v __attribute__((ext_vector_type(2)));
         typedef double d8v __attribute__((ext_vector_type(8)));
         const f2v pr = {sc0, sc0};
@@ -900,7 +923,14 @@ void attention32_kernel(AttnArgs a) {
           asm("v_mov_b64 %0, %1 ; %2" : "=v"(t) : "v"(dp), "n"(i));
           dv[i] = t;
         }
-        sc[nb] = __builtin_bit_cast(f16v, dv);
+        cinit = __builtin_bit_cast(f16v, dv);
+      }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      if (EDGE && nb >= nbv) break;
+      if constexpr (PS && STEADY) {
+        sc[nb] = cinit;
       } else {
 #pragma unroll
         for (int e = 0; e < 16; ++e) sc[nb][e] = sc0;
@@ -958,10 +988,12 @@ void attention32_kernel(AttnArgs a) {
         const bool shift_row = is_fresh ? (full > -INFINITY) : (full - mrow > kRescaleLog2);
         float alpha = 1.f;
         if (shift_row) {
-          if (!is_fresh) alpha = __builtin_amdgcn_exp2f(mrow - full);
-          mrow = full;
+          const float mnew = round_m(full);
+          if (!is_fresh) alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+          mrow = mnew;
           fresh = false;
         }
+        set_mneg();  // all lanes (the ballot inside needs the whole wave)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
         // the row sums of queries (l % 16) and (l % 16) + 16 live in lanes 0..15
@@ -1066,10 +1098,12 @@ void attention32_kernel(AttnArgs a) {
         const bool shift_row = is_fresh ? (full > -INFINITY) : (full - mrow > kRescaleLog2);
         float alpha = 1.f;
         if (shift_row) {
-          if (!is_fresh) alpha = __builtin_amdgcn_exp2f(mrow - full);
-          mrow = full;
+          const float mnew = round_m(full);
+          if (!is_fresh) alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+          mrow = mnew;
           fresh = false;
         }
+        set_mneg();  // all lanes (the ballot inside needs the whole wave)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
         const float a0 = __shfl(alpha, l & 15), a1 = __shfl(alpha, (l & 15) + 16);
