@@ -86,7 +86,10 @@ int mpk_linear_residual(const void* x, int x_dtype, const void* w, const void* b
  *   residual_out = fp16(x) * w^T + b + residual          (FP32)
  *   normalized_out = LayerNorm(residual_out) * gamma + beta
  * x: [m, d] in x_dtype; w: [d, d] FP16; b: [d] FP16; residual, residual_out:
- * [m, d] FP32; gamma, beta: [d] FP32.  d in {32, 64, 128, 256, 512}.
+ * [m, d] FP32; gamma, beta: [d] FP32.  d in {32, 64, 128, 256, 512}.  variant: 0 (built-in
+ * choice), 1 / 2 (whole rows per wave on LDS-staged tiles), 3 (large tiles holding whole rows,
+ * d 256 / 512), 4 (d 256 with FP16 x: the weights resident in LDS, independent 16-row wave
+ * tiles; bit-identical to 1 and 2).
  * Replaces: mixed_linear_add_layer_norm (mixed_precision/triton_linear.py:272-324).
  */
 int mpk_linear_residual_layernorm(const void* x, int x_dtype, const void* w, const void* b,

@@ -245,6 +245,33 @@ def test_linear_residual_layernorm(hip_device, d, m, variant):
             _close(n_out, _ln64(r64, norm), tol, tol, "normalized_out")
 
 
+@pytest.mark.parametrize("m", [5, 16, 1000, 70001])
+def test_linear_layernorm_resident_variant(hip_device, m):
+    """Variant 4 (d = K = 256, FP16 X: weights resident in LDS, independent 16-row wave tiles)
+    equals variant 1 (the same fragments, MFMA order and epilogue on LDS-staged tiles) bit for
+    bit, FP16 and FP32 normalized outputs, ragged row counts and more tiles than waves; FP32 X
+    is rejected."""
+    from tiktoktechjam2026_amd import _ops
+
+    d = 256
+    lin = _linear(d, d, hip_device, 31)
+    norm = _norm(d, hip_device, 32)
+    x = _randn((m, d), 33).to(hip_device, torch.float16)
+    resid = _randn((m, d), 34, 2.0).to(hip_device)
+    for out_code in (0, 1):
+        r1, n1 = _ops.linear_residual_layer_norm(x, lin.weight, lin.bias, resid, norm.weight, norm.bias,
+                                                 float(norm.eps), out_code, 1)
+        r4, n4 = _ops.linear_residual_layer_norm(x, lin.weight, lin.bias, resid, norm.weight, norm.bias,
+                                                 float(norm.eps), out_code, 4)
+        assert torch.equal(r1, r4) and torch.equal(n1, n4), out_code
+    r64 = _ref_linear(x.float().cpu(), lin, False) + resid.double().cpu()
+    _close(r4, r64, 2e-5 * math.sqrt(d), 1e-6, "resident residual_out")
+    _close(n4, _ln64(r64, norm), 2 ** -10, 2 ** -10, "resident normalized_out (FP16)")
+    with pytest.raises(RuntimeError):
+        _ops.linear_residual_layer_norm(x.float(), lin.weight, lin.bias, resid, norm.weight, norm.bias,
+                                        float(norm.eps), 1, 4)
+
+
 @pytest.mark.parametrize("n,k", [(256, 256), (256, 1024), (256, 136), (512, 512), (512, 2048), (512, 40)])
 @pytest.mark.parametrize("m", [7, 300, 5000, 256 * 128 + 77])
 def test_linear_residual_layer_norm_wide(hip_device, n, k, m):

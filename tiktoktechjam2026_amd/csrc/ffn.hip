@@ -185,6 +185,7 @@ __global__ __launch_bounds__(kBlock) void ffn_ln_kernel(FfnArgs a) {
           load8_f32(a.beta + n, bt);
 #pragma unroll
           for (int j = 0; j < 8; ++j) o[j] = (v[j] - mean) * rstd * gm[j] + bt[j];
+          pin_f32x8(o);  // rounded to FP32, then to the output type (no fused FMA + conversion)
           store8(NO + m * D + n, o);
         }
       }

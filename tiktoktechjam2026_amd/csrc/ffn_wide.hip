@@ -398,6 +398,7 @@ __global__ __launch_bounds__(kNT, 1) void ffn_wide_kernel(FfnArgs a) {
         float o[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = (yacc[p][8 * r + j] - mean) * rstd * gm[n + j] + bt[n + j];
+        pin_f32x8(o);  // rounded to FP32, then to the output type (no fused FMA + conversion)
         buffer_store8(no, (uint32_t)((li * D + n) * sizeof(OT)), o, static_cast<OT*>(a.normalized_out));
       }
   }
@@ -761,6 +762,7 @@ __global__ __launch_bounds__(kRT) void ffn_roles_kernel(FfnArgs a) {
         float o[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = (yacc[p][8 * r + j] - mean) * rstd * gm[n + j] + bt[n + j];
+        pin_f32x8(o);  // rounded to FP32, then to the output type (no fused FMA + conversion)
         buffer_store8(no, base_o + (uint32_t)((32 * p + 16 * r) * sizeof(OT)), o, static_cast<OT*>(a.normalized_out));
       }
 #pragma unroll

@@ -801,10 +801,14 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
         float mean, rstd;
         row_stats<PN>(xr[t], inv_d, a.eps2, mean, rstd);
 #pragma unroll
-        for (int p = 0; p < PN; ++p)
+        for (int p = 0; p < PN; ++p) {
+          float o[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-            n2f[t][p][j] = (_Float16)((xr[t][p][j] - mean) * rstd * gm[p][j] + bt[p][j]);
+          for (int j = 0; j < 8; ++j) o[j] = (xr[t][p][j] - mean) * rstd * gm[p][j] + bt[p][j];
+          pin_f32x8(o);  // rounded to FP32, then to the output type (no fused FMA + conversion)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) n2f[t][p][j] = (_Float16)o[j];
+        }
       }
 
       // ---- FFN: x'' = x' + Wout fp16(GELU(Win n2 + bin)) + bout ----
@@ -908,6 +912,7 @@ __global__ __launch_bounds__(64 * W) void layer_tail_kernel(TailArgs a) {
         float o[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = (xr[t][p][j] - mean) * rstd * gm[p][j] + bt[p][j];
+        pin_f32x8(o);  // rounded to FP32, then to the output type (no fused FMA + conversion)
         if constexpr (LAST) {
           buffer_store8(ores, (uint32_t)((16 * t + r) * D + n) * 4u, o, static_cast<float*>(a.out));
         } else {

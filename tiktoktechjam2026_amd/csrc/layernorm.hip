@@ -90,6 +90,7 @@ __global__ __launch_bounds__(kBlock) void residual_layernorm_kernel(
         o[1] = (r[k][v].y - mean) * rstd * gm.y + bt.y;
         o[2] = (r[k][v].z - mean) * rstd * gm.z + bt.z;
         o[3] = (r[k][v].w - mean) * rstd * gm.w + bt.w;
+        pin_f32x4(o);  // rounded to FP32, then to the output type (no fused FMA + conversion)
         OT* dst = norm_out + row * d + 4 * c;
         if constexpr (sizeof(OT) == 4) {
           const f4 v = {o[0], o[1], o[2], o[3]};
