@@ -945,10 +945,8 @@ __global__ __launch_bounds__(64 * kResWaves) void linear_ln_resident_kernel(Line
     }
     // R' = acc + b + R ; N' = LayerNorm(R') (whole rows: lane r holds row r's features
     // 32 p + 8 g .. +7, the four lane groups g the rest)
-    const int64_t m = tile * 16 + r;
     const uint32_t rows = (uint32_t)max<int64_t>(0, min<int64_t>(16, M - tile * 16));
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.residual + tile * 16 * D, rows * (uint32_t)(D * 4));
-    (void)m;
     // pass 1: R' in place of the accumulators (the residual read through a buffer
     // resource bounded by the rows that exist), row sums
     float sum = 0.f;
