@@ -160,3 +160,24 @@ def test_attention_in_layer_tail_route():
     assert not dispatch.plan(TransformerConfig(2, 64, 64, 1, 64, 2, True)).fuse_attention_tail  # hd 64
     for (d, hd) in dispatch.ATTENTION_TAIL_ROUTE_MAX_SEQ:
         assert any(dispatch.attention_tail_supported(d, f, d // hd) for (dd, f) in dispatch.LAYER_TAIL_SHAPES if dd == d)
+
+
+def test_prescaled_q_route():
+    """Head dim 32 from 256 keys runs the pre-scaled attention wherever the attention is a launch of
+    its own (its producers scale q): cfg2 (layer-tail route) and cfg5 (GEMM route); cfg1 (128 keys:
+    the 16x16 kernel), cfg3 (attention inside the layer tail), cfg4 (head dim 64) and forced
+    16x16 variants keep the scaling kernel."""
+    from dataclasses import replace
+
+    routes = {name: dispatch.plan(cfg) for name, cfg in BENCHMARK_CONFIGS.items()}
+    chosen = {}
+    for name, cfg in BENCHMARK_CONFIGS.items():
+        route = routes[name]
+        in_tail = route.fuse_layer_tail and dispatch.attention_tail_for(route, cfg.seq_len, masked=False)
+        chosen[name] = not in_tail and dispatch.prescaled_attention_for(route, cfg.seq_len)
+    assert chosen == {"cfg1": False, "cfg2": True, "cfg3": False, "cfg4": False, "cfg5": True}
+    cfg5 = routes["cfg5"]
+    assert not dispatch.prescaled_attention_for(cfg5, dispatch.PRESCALED_ATTENTION_MIN_SEQ - 1)
+    assert not dispatch.prescaled_attention_for(replace(cfg5, attention_variant=1), 4096)
+    assert dispatch.prescaled_attention_for(replace(cfg5, attention_variant=7), 4096)
+    assert not dispatch.prescaled_attention_for(replace(cfg5, prescale_q=False), 4096)
