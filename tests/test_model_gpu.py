@@ -211,8 +211,13 @@ def test_forward_into_out_is_exact(hip_device, config, padding):
             model(x, mask, out=torch.empty_like(x, dtype=torch.float16))
 
 
-def test_hip_graph_replays_match_eager(hip_device):
-    config = TransformerConfig(8, 128, 128, 4, 128, 2, True)
+@pytest.mark.parametrize("config", [
+    TransformerConfig(8, 128, 128, 4, 128, 2, True),   # layer-tail route
+    TransformerConfig(4, 512, 128, 4, 128, 2, True),   # layer-tail route, q pre-scaled by the tail
+    TransformerConfig(2, 512, 256, 8, 512, 2, True),   # GEMM route, q pre-scaled by the projection
+    TransformerConfig(8, 128, 64, 2, 128, 2, True),    # attention inside the layer tail
+], ids=["tail", "tail_prescaled", "gemm_prescaled", "attention_in_tail"])
+def test_hip_graph_replays_match_eager(hip_device, config):
     _, model = _build(config, hip_device)
     graphed = harness.HipGraphModel(model)
     for seed in range(4):
