@@ -17,7 +17,8 @@ pytestmark = pytest.mark.gpu
 
 CASES = {
     "cfg1": BENCHMARK_CONFIGS["cfg1"],                   # layer-tail route
-    "d256": TransformerConfig(4, 256, 256, 8, 1024, 2, True),  # GEMM route with LayerNorm epilogues
+    "d256": TransformerConfig(4, 256, 256, 8, 1024, 2, True),  # GEMM route with LayerNorm epilogues, q pre-scaled
+    "d128_s512": TransformerConfig(2, 512, 128, 4, 128, 2, True),  # layer-tail route, q pre-scaled by the tail
 }
 
 
