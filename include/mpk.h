@@ -55,6 +55,9 @@ int mpk_layernorm(const float* x, const float* update, const float* gamma, const
  * Projection y = act(fp16(x) * w^T + b), FP32 accumulate, act = exact-erf GELU
  * when gelu != 0.  x: [m, k] in x_dtype; w: [n, k] FP16 (nn.Linear layout);
  * b: [n] FP16; y: [m, n] in y_dtype.  n % 8 == 0, k % 8 == 0.
+ * variant 0: the built-in table (mpk_linear_auto_variant); 1-9 pin a tile shape (all give
+ * identical results).  8: 256x256 tiles with LDS-DMA operand staging; 9: X-stationary
+ * 256-token tiles with W streamed through LDS (FP16 x, k = 128 or 256, n % 64 == 0).
  * Replaces: mixed_linear (mixed_precision/triton_linear.py:221-269).
  */
 int mpk_linear(const void* x, int x_dtype, const void* w, const void* b, void* y, int y_dtype, int gelu,

@@ -145,6 +145,32 @@ def test_linear_large_tile_variants_bit_identical(hip_device, m, n, k):
             assert torch.equal(y7, y8), f"out={out_dtype} gelu={gelu}"
 
 
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(70000, 768, 256), (1, 768, 256), (255, 512, 256), (257, 384, 128), (3000, 256, 128), (4113, 1024, 256),
+     (262244, 768, 256)],
+)
+def test_linear_x_stationary_variant_bit_identical(hip_device, m, n, k):
+    """Variant 9 (X rows in registers, W streamed in 64-row blocks) accumulates the same
+    MFMAs in the same order as variant 8: identical outputs for ragged M, tiles per workgroup
+    from 1 to 5, N / 64 equal to and above K / 32, both epilogues, the q-scaled form, and
+    FP16 / FP32 outputs."""
+    from tiktoktechjam2026_amd.mixed_precision.hip_linear import mixed_linear, mixed_linear_q_scaled
+
+    print(f"\n[linear 8/9] m={m} n={n} k={k}", flush=True)
+    lin = _linear(k, n, hip_device, 37)
+    x = _randn((m, k), 41).to(hip_device, torch.float16)
+    combos = [(torch.float16, False)] if m > 100000 else [(o, g) for o in (torch.float32, torch.float16) for g in (False, True)]
+    for out_dtype, gelu in combos:
+        y8, y9 = (mixed_linear(x, lin, output_dtype=out_dtype, fuse_gelu=gelu, variant=v) for v in (8, 9))
+        assert torch.equal(y8, y9), f"out={out_dtype} gelu={gelu}"
+    q8, q9 = (mixed_linear_q_scaled(x, lin, k, 0.25503486, variant=v) for v in (8, 9))
+    assert torch.equal(q8, q9)
+    plain = mixed_linear(x, lin, output_dtype=torch.float32, variant=9)
+    _close(plain[:64], _ref_linear(x[:64], lin, False), 1e-5 * math.sqrt(k), 1e-5 * math.sqrt(k),
+           "variant 9 against the float64 reference")
+
+
 @pytest.mark.parametrize("n,variant", [(8, 0), (256, 7), (128, 1)])
 def test_gelu_epilogue_accuracy(hip_device, n, variant):
     """The GEMM's GELU alone: X = [v, 0, ...] and W[:, 0] = 1 make every pre-activation
@@ -903,7 +929,7 @@ def test_attention_layer_tail_rejects(hip_device):
 
 
 @pytest.mark.parametrize("m,n,k,q_cols", [(130, 768, 256, 256), (8192, 384, 128, 128), (257, 40, 24, 16), (64, 96, 32, 0)])
-@pytest.mark.parametrize("variant", [0, 1, 5, 7, 8])
+@pytest.mark.parametrize("variant", [0, 1, 5, 7, 8, 9])
 def test_linear_q_scaled(hip_device, m, n, k, q_cols, variant):
     """The QKV projection with the attention scale folded into q: columns from q_cols on equal
     mpk_linear's bit for bit (the same kernel, times 1), the first q_cols are (x W^T + b) * c

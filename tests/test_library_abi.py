@@ -53,7 +53,7 @@ def test_host_side_argument_rejection(built_library):
     assert lib.mpk_linear(fake, 7, fake, fake, fake, 1, 0, 10, 16, 16, 0, null) == _lib.MPK_EINVAL
     assert lib.mpk_linear(fake, 1, fake, fake, fake, 1, 0, 10, 12, 16, 0, null) == _lib.MPK_EUNSUPPORTED
     assert lib.mpk_linear(ctypes.c_void_p(72), 1, fake, fake, fake, 1, 0, 10, 16, 16, 0, null) == _lib.MPK_EALIGN
-    assert lib.mpk_linear(fake, 1, fake, fake, fake, 1, 0, 10, 16, 16, 9, null) == _lib.MPK_EUNSUPPORTED
+    assert lib.mpk_linear(fake, 1, fake, fake, fake, 1, 0, 10, 16, 16, 10, null) == _lib.MPK_EUNSUPPORTED
     assert lib.mpk_linear_residual(fake, 1, fake, fake, null, fake, 10, 16, 16, 0, null) == _lib.MPK_EINVAL
     assert lib.mpk_linear_residual(fake, 1, fake, fake, fake, fake, 10, 20, 16, 0, null) == _lib.MPK_EUNSUPPORTED
     assert lib.mpk_linear_residual(fake, 1, fake, fake, ctypes.c_void_p(72), fake, 10, 16, 16, 0, null) == _lib.MPK_EALIGN
@@ -100,7 +100,12 @@ def test_host_side_argument_rejection(built_library):
 
 def test_auto_variant_queries(built_library):
     lib = built_library
-    assert lib.mpk_linear_auto_variant(65536, 384, 128) in (1, 2, 3, 4)
+    # the X-stationary tiles for K = 128 / 256 from 256 workgroup tiles (65,536 rows) on
+    assert lib.mpk_linear_auto_variant(65536, 384, 128) == 9
+    assert lib.mpk_linear_auto_variant(262144, 768, 256) == 9
+    assert lib.mpk_linear_auto_variant(65535, 768, 256) == 8
+    assert lib.mpk_linear_auto_variant(65536, 320, 256) in (1, 2, 3, 4)  # N / 64 < K / 32
+    assert lib.mpk_linear_auto_variant(32768, 1536, 512) == 8
     assert lib.mpk_linear_residual_layernorm_auto_variant(65536, 128) in (1, 2)
     assert lib.mpk_linear_residual_layernorm_auto_variant(262144, 256) == 3
     assert lib.mpk_ffn_residual_layernorm_auto_variant(65536, 128, 128) in (1, 2)

@@ -35,6 +35,9 @@ def test_roles_of_current_kernel_templates():
            "_ZN3mpk17linear_dma_kernelILi3EfEEvNS_10LinearArgsE"]
     assert profiling.parse_kernel_name(dma[2]) == ("linear_dma_kernel", ["3", "float"])
     assert [profiling.base_kernel_key(n) for n in dma] == ["qkv_proj", "ffn_in", "@residual"]
+    xs = ["_ZN3mpk16linear_xs_kernelILi8ELi0EDF16_EEvNS_10LinearArgsE", "_ZN3mpk16linear_xs_kernelILi4ELi1EfEEvNS_10LinearArgsE"]
+    assert profiling.parse_kernel_name(xs[1]) == ("linear_xs_kernel", ["4", "1", "float"])
+    assert [profiling.base_kernel_key(n) for n in xs] == ["qkv_proj", "ffn_in"]
 
 
 def test_parse_mangled_and_demangled_names():

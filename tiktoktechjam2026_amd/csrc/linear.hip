@@ -868,6 +868,256 @@ static hipError_t launch_linear_dma(const LinearArgs& a, hipStream_t s) {
   return launch_linear_big<256, 256, 64, 2, XT, EPI, OT>(a, s);
 }
 
+// ---- X-stationary projection (FP16 X, K = 128 or 256, N % 64 == 0) ----
+// For projections with a short K (the d_model-256 QKV projection: 262,144 x 768 x 256),
+// each wave keeps its 32 tokens' whole X rows as MFMA fragments in registers (K = 256:
+// 64 VGPRs, and as many again for the next tile's rows, loaded one k-step pair per step
+// during the current tile's first steps) while the workgroup streams W through LDS in
+// 64-row blocks, one block per step.  A step multiplies the workgroup's 256 tokens by the
+// block and stores the 256 x 64 results at once: outputs leave as a steady stream of whole
+// 128-byte lines (a lane's 8 consecutive features x the four lane groups x the two 32-row
+// halves of the block) instead of the large tiles' bursts at tile ends.
+//
+// The products are those of every other variant - 16x16x32 MFMAs, k-steps in increasing
+// order from zero, then bias (and GELU or the q scale) in FP32 - so the results are
+// bit-identical to them.  W blocks travel global -> LDS by LDS-DMA copies two steps ahead
+// through a ring of three stages; a staged row is K + 16 halves (an odd multiple of 32
+// bytes: conflict-free fragment reads) and slot S of a block holds W row
+// 32 (S / 32) + pair_row(S % 16, (S / 16) % 2), so lane r of a fragment reads slot r and
+// a lane's outputs are 8 consecutive features.  One barrier per step.  Completion is
+// tracked by count as in linear_dma_kernel: at the end of step s a wave waits until its
+// copies of step s - 1 (the block of step s + 1) have landed, allowing the X loads and
+// stores of step s - 1 and the copies, X loads and stores of step s to stay in flight.
+constexpr int kXsWaves = 8;
+constexpr int kXsTile = 32 * kXsWaves;  // tokens per workgroup tile
+constexpr int kXsRows = 64;             // W rows (output features) per step
+
+// f(integral_constant<int, I>) for I = B .. E - 1, in order
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+template <int KS>
+struct XsShape {
+  static constexpr int K = 32 * KS;
+  static constexpr int RU = K / 8 + 2;                            // 16-byte units per staged row
+  static constexpr int BLOCKS = RU;                               // 1-KB copies per step (64 RU units)
+  static constexpr int CPW = (BLOCKS + kXsWaves - 1) / kXsWaves;  // copy slots per wave
+  static constexpr int STAGE = BLOCKS * 1024;                     // bytes per ring stage
+  static constexpr int NS = 3;
+  static_assert(kXsRows * RU == 64 * BLOCKS, "whole copies");
+};
+
+template <int KS, int EPI, typename OT>
+__global__ __launch_bounds__(64 * kXsWaves) void linear_xs_kernel(LinearArgs a) {
+  using SH = XsShape<KS>;
+  constexpr int K = SH::K, CPW = SH::CPW;
+  constexpr int STORES = 4 * (sizeof(OT) == 4 ? 2 : 1);  // store instructions per wave and step
+  static_assert(EPI == kEpiBias || EPI == kEpiBiasGelu, "plain epilogues");
+  __shared__ __align__(16) unsigned char stages[SH::NS * SH::STAGE + 1024];  // + slack for surplus copies
+  __shared__ __align__(16) _Float16 bias_s[kDmaMaxN];
+
+  const _Float16* __restrict__ X = static_cast<const _Float16*>(a.x);
+  const _Float16* __restrict__ W = a.w;
+  const int64_t M = a.m;
+  const int N = a.n;
+  const int NC = N / kXsRows;  // steps per tile (>= KS, checked by the launcher)
+  const int64_t ntiles = (M + kXsTile - 1) / kXsTile;
+  const int64_t tile0 = blockIdx.x;
+  if (tile0 >= ntiles) return;  // uniform per workgroup, before any barrier
+  const int my_tiles = (int)((ntiles - 1 - tile0) / gridDim.x) + 1;
+
+  const int l = threadIdx.x & 63, wave = wave_id();
+  const int r = l & 15, g = l >> 4;
+
+  for (int i = 8 * (int)threadIdx.x; i < N; i += 8 * 64 * kXsWaves)
+    *reinterpret_cast<h8*>(&bias_s[i]) = *reinterpret_cast<const h8*>(a.bias + i);
+
+  // ---- copies: slot j of this wave copies block wave + 8 j of a step's W rows ----
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)stages;
+  uint32_t coff[CPW], cdst[CPW], cstage[CPW];
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) {
+    const int b = wave + kXsWaves * j;
+    if (b < SH::BLOCKS) {
+      const int u = 64 * b + l, slot = u / SH::RU, pos = u % SH::RU;
+      const int row = 32 * (slot >> 5) + pair_row(slot & 15, (slot >> 4) & 1);
+      coff[j] = pos < K / 8 ? (uint32_t)(row * K + 8 * pos) * 2u : 0u;  // pad units copy element 0
+      cdst[j] = lds0 + (uint32_t)(b * 1024);
+      cstage[j] = (uint32_t)SH::STAGE;
+    } else {
+      coff[j] = 0u;
+      cdst[j] = lds0 + (uint32_t)(SH::NS * SH::STAGE);  // slack: written, never read
+      cstage[j] = 0u;
+    }
+  }
+  // copy slot j of the W block of tile-step c into ring stage st
+  auto copy = [&](int j, int c, int st) {
+    dma16(coff[j], W + (int64_t)(kXsRows * c) * K, cdst[j] + (uint32_t)st * cstage[j]);
+  };
+
+  // ---- X fragments: [t][ks] = token 16 t + r of the wave's 32, k = 32 ks + 8 g .. + 7 ----
+  const uint32_t xoff = (uint32_t)(r * K + 8 * g) * 2u;
+  auto x_rsrc = [&](int tile_i) {
+    const int64_t row0 = (tile0 + (int64_t)tile_i * gridDim.x) * kXsTile + 32 * wave;
+    const uint32_t rows = (uint32_t)max<int64_t>(0, min<int64_t>(32, M - row0));
+    return make_rsrc(X + row0 * K, rows * (uint32_t)(K * 2));
+  };
+  h8 xa[2][KS], xb[2][KS];
+
+  // ---- prologue: the first tile's X, the W blocks of steps 0 and 1 ----
+  {
+    const __amdgpu_buffer_rsrc_t xr = x_rsrc(0);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        xa[t][ks] = buffer_load8_as_half(xr, xoff + (uint32_t)((16 * t * K + 32 * ks) * 2), X);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) copy(j, q % NC, q);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  OT* Y = static_cast<OT*>(a.y);
+  int st = 0;  // ring stage of the current step
+  // One step: tile-step c of a tile, multiplying the X fragments xc; XI >= 0: the step also
+  // loads k-step pair XI of the next tile's X into xn (through a zero-size resource, so
+  // without memory traffic, when there is no next tile: the loads stay unconditional and
+  // land in xn's own registers).  XPREV: X loads of the step before (-1: decided at run
+  // time, for a tile's first step).
+  auto step = [&](int c, auto xi_tag, auto xprev_tag, bool prev_loaded, const __amdgpu_buffer_rsrc_t& yr,
+                  const __amdgpu_buffer_rsrc_t& xr, h8 (&xc)[2][KS], h8 (&xn)[2][KS]) {
+    constexpr int XI = decltype(xi_tag)::value;
+    constexpr int XPREV = decltype(xprev_tag)::value;
+    // the block of step s + 2 (past the end: a block that nobody reads again)
+    const int st2 = st == 0 ? 2 : st - 1;
+    const int c2 = c + 2 < NC ? c + 2 : c + 2 - NC;
+    const unsigned char* sp = stages + st * SH::STAGE + (r * SH::RU + g) * 16;
+    f4 acc[2][2][2];  // [p][tt][t]
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[p][tt][t] = zero4();
+    h8 wf[2][2][2];  // [k-step parity][p][tt]
+    auto read_w = [&](int ks, h8 (&w)[2][2]) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+          w[p][tt] = *reinterpret_cast<const h8*>(sp + ((32 * p + 16 * tt) * SH::RU + 4 * ks) * 16);
+    };
+    read_w(0, wf[0]);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) read_w(ks + 1, wf[(ks + 1) & 1]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) acc[p][tt][t] = mfma32(wf[ks & 1][p][tt], xc[t][ks], acc[p][tt][t]);
+      if (ks < CPW) copy(ks, c2, st2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int j = KS; j < CPW; ++j) copy(j, c2, st2);
+    constexpr int XL = XI >= 0 ? 2 : 0;
+    if constexpr (XI >= 0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        xn[t][XI] = buffer_load8_as_half(xr, xoff + (uint32_t)((16 * t * K + 32 * XI) * 2), X);
+    }
+    // epilogue: + bias (+ GELU | q scale), a row's two 64-byte runs back to back
+    const int nb = kXsRows * c + 8 * g;
+    h8 bh[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) bh[p] = *reinterpret_cast<const h8*>(&bias_s[nb + 32 * p]);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = acc[p][0][t][i] + (float)bh[p][i];
+          v[4 + i] = acc[p][1][t][i] + (float)bh[p][4 + i];
+        }
+        if constexpr (EPI == kEpiBiasGelu) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = gelu_erf(v[j]);
+        }
+        if constexpr (EPI == kEpiBias) q_scale8(a, nb + 32 * p, v);
+        buffer_store8(yr, (uint32_t)((16 * t + r) * N + nb + 32 * p) * (uint32_t)sizeof(OT), v, Y);
+      }
+    // this wave's copies of the block of step s + 1 (issued in step s - 1) have landed
+    constexpr int BASE = 2 * STORES + CPW + XL;
+    if constexpr (XPREV >= 0) {
+      wait_copies<BASE + XPREV>();
+    } else {
+      if (prev_loaded) wait_copies<BASE + 2>();
+      else wait_copies<BASE>();
+    }
+    lds_barrier();
+    st = st == 2 ? 0 : st + 1;
+  };
+  using NoX = std::integral_constant<int, -1>;
+  // One tile: steps 0 .. KS - 1 unrolled (each loads one k-step pair of the next tile's X),
+  // then the rest as a loop.  A tile's first step follows the previous tile's last, which
+  // loaded X only when NC == KS.
+  auto run_tile = [&](int tile_i, h8 (&xc)[2][KS], h8 (&xn)[2][KS]) {
+    const bool has_next = tile_i + 1 < my_tiles;
+    const int64_t row0 = (tile0 + (int64_t)tile_i * gridDim.x) * kXsTile + 32 * wave;
+    const uint32_t rows = (uint32_t)max<int64_t>(0, min<int64_t>(32, M - row0));
+    const __amdgpu_buffer_rsrc_t yr = make_rsrc(Y + row0 * N, rows * (uint32_t)N * (uint32_t)sizeof(OT));
+    const __amdgpu_buffer_rsrc_t xr = has_next ? x_rsrc(tile_i + 1) : make_rsrc(X, 0u);
+    const bool first_prev = tile_i > 0 && NC == KS;
+    static_for<0, KS>([&](auto i_tag) {
+      constexpr int I = decltype(i_tag)::value;
+      step(I, i_tag, std::integral_constant<int, I == 0 ? -1 : 2>{}, first_prev, yr, xr, xc, xn);
+    });
+#pragma unroll 1
+    for (int c = KS; c < NC; ++c) step(c, NoX{}, NoX{}, c == KS, yr, xr, xc, xn);
+  };
+#pragma unroll 1
+  for (int tile_i = 0; tile_i < my_tiles; tile_i += 2) {
+    run_tile(tile_i, xa, xb);
+    if (tile_i + 1 >= my_tiles) break;
+    run_tile(tile_i + 1, xb, xa);
+  }
+  wait_copies<0>();  // no copy may land in LDS after the workgroup has left it
+}
+
+// Variant 9: FP16 X, K = 128 or 256, N % 64 == 0 with N / 64 >= K / 32, bias or bias + GELU
+// epilogue runs linear_xs_kernel; other inputs run variant 8.
+template <typename XT, int EPI, typename OT>
+static hipError_t launch_linear_xs(const LinearArgs& a, hipStream_t s) {
+  constexpr bool kOk = std::is_same<XT, _Float16>::value && (EPI == kEpiBias || EPI == kEpiBiasGelu);
+  if constexpr (kOk) {
+    const int ks = a.k / 32;
+    if ((a.k == 128 || a.k == 256) && a.n % kXsRows == 0 && a.n / kXsRows >= ks && a.n <= kDmaMaxN &&
+        a.m <= ((int64_t)1 << 40)) {
+      const int64_t ntiles = (a.m + kXsTile - 1) / kXsTile;
+      auto launch = [&](auto kernel) {
+        const int64_t grid = std::min<int64_t>(ntiles, resident_grid(kernel, 64 * kXsWaves, 0));
+        hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(64 * kXsWaves), 0, s, a);
+        return hipGetLastError();
+      };
+      if (a.k == 256) return launch(linear_xs_kernel<8, EPI, OT>);
+      return launch(linear_xs_kernel<4, EPI, OT>);
+    }
+  }
+  return launch_linear_dma<XT, EPI, OT>(a, s);
+}
+
 // ---- projection + residual + LayerNorm with the weights resident in LDS (d = K = 256) ----
 // linear_kernel's whole-row LayerNorm variant (same fragments, MFMA order and epilogue
 // arithmetic, so the results are bit-identical to variants 1 and 2) restructured for
@@ -1030,6 +1280,8 @@ static hipError_t launch_linear(const LinearArgs& a, hipStream_t s) {
 //   6: as 5 with single-buffered LDS (two workgroups per CU)
 //   7: BM256 BN256 (2x4 waves, 128x64 per wave, double-buffered LDS)
 //   8: as 7 with LDS-DMA operand staging (FP16 X; other inputs run 7)
+//   9: X-stationary 256-token tiles, W streamed in 64-row blocks (FP16 X, K = 128 or 256,
+//      N % 64 == 0, bias / GELU epilogues; other inputs run 8)
 template <typename XT, int EPI, typename OT>
 static hipError_t linear_variant(int variant, const LinearArgs& a, hipStream_t s) {
   switch (variant) {
@@ -1041,6 +1293,7 @@ static hipError_t linear_variant(int variant, const LinearArgs& a, hipStream_t s
     case 6: return launch_linear_big<256, 128, 64, 1, XT, EPI, OT>(a, s);
     case 7: return launch_linear_big<256, 256, 64, 2, XT, EPI, OT>(a, s);
     case 8: return launch_linear_dma<XT, EPI, OT>(a, s);
+    case 9: return launch_linear_xs<XT, EPI, OT>(a, s);
     default: return (hipError_t)MPK_EUNSUPPORTED;
   }
 }
@@ -1088,6 +1341,10 @@ using namespace mpk;
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 extern "C" int mpk_linear_auto_variant(int64_t m, int32_t n, int32_t k) {
+  // X-stationary tiles from 256 workgroup tiles on (measured on MI355X with the q-scaled
+  // bias epilogue: 262,144 x 768 x 256 in 142 vs 170 us for variant 8, 65,536 x 768 x 256
+  // 39 vs 42 us, 65,536 x 384 x 128 17.6 vs 21.4 us)
+  if ((k == 128 || k == 256) && n % 64 == 0 && n / 64 >= k / 32 && n <= 8192 && m >= (int64_t)256 * 256) return 9;
   if (n % 256 == 0 && k >= 256 && k <= (1 << 20) && ((m + 255) / 256) * (n / 256) >= 256) return 8;
   if (n % 128 == 0 && m >= 128 * 256) return 1;
   if (n % 128 == 0) return 4;

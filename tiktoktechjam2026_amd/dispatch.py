@@ -48,6 +48,9 @@ kernel sources for the exact tiles):
                               through registers into LDS
                            8: as 7 with LDS-DMA operand staging (four-stage ring; FP16 X,
                               K % 32 == 0, K >= 128; others run 7) - the wide-model choice
+                           9: X-stationary 256-token tiles, W streamed in 64-row blocks (FP16
+                              X, K = 128 / 256, N % 64 == 0, bias or GELU epilogue; others run
+                              8) - the choice for those K from 65,536 rows
   out-proj + LN (mpk_linear_residual_layernorm)
                            1: 64 rows/WG           2: 128 rows/WG (row-owning waves, d <= 128)
                            3: GEMM tiles holding whole rows with a cross-wave LayerNorm

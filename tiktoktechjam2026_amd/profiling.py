@@ -404,6 +404,10 @@ def base_kernel_key(name: str) -> str:
         # linear_dma_kernel<EPI, OT>: the epilogue is the first template argument
         epi = int(args[0]) if args and args[0].lstrip("-").isdigit() else -1
         return {0: "qkv_proj", 1: "ffn_in", 3: "@residual"}.get(epi, "linear")
+    if base == "linear_xs_kernel":
+        # linear_xs_kernel<KS, EPI, OT>: the epilogue is the second template argument
+        epi = int(args[1]) if len(args) > 1 and args[1].lstrip("-").isdigit() else -1
+        return {0: "qkv_proj", 1: "ffn_in"}.get(epi, "linear")
     if base in ("ffn_ln_kernel", "ffn_wide_kernel", "ffn_roles_kernel"):
         return "ffn_ln"
     if base == "residual_layernorm_kernel":
