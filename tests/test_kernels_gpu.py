@@ -237,7 +237,7 @@ def test_mixed_linear_residual_rejects_bad_inputs(hip_device):
     with pytest.raises(ValueError):
         mixed_linear_residual(x, lin, x, out=torch.zeros(10, 64, device=hip_device, dtype=torch.float16))
     with pytest.raises(RuntimeError):
-        mixed_linear_residual(x, lin, x, variant=9)
+        mixed_linear_residual(x, lin, x, variant=10)
 
 
 def test_mixed_linear_3d_input(hip_device):

@@ -658,11 +658,11 @@ void attention32_kernel(AttnArgs a) {
   const int BH = a.batch * a.heads;
   const int nqb = (S + QB - 1) / QB;
   // As in attention_kernel, each XCD owns a contiguous range of (batch, head) rows.  When
-  // the launch runs many rounds of workgroups (group > 0, set by the launcher), the rows are
-  // instead walked in groups of `group` rows, one group per XCD at a time, each group's query
-  // blocks longest first: the workgroups in flight on an XCD then share the K/V prefixes of
-  // about `group` rows, which fit its L2 (at B 64, H 8, S 4096, hd 32 the fetched bytes drop
-  // from 2.41 GB to 0.59 GB per launch).  Otherwise the XCD runs one query block of every row of its range at a
+  // the launch runs many rounds of workgroups (group > 0, set by the launcher), the XCD walks
+  // its range in groups of `group` rows, each group's query blocks longest first: the
+  // workgroups in flight on an XCD then share the K/V prefixes of about `group` rows, which
+  // fit its L2 (at B 64, H 8, S 4096, hd 32 the fetched bytes drop from 2.41 GB to 0.59 GB
+  // per launch).  Otherwise the XCD runs one query block of every row of its range at a
   // time, longest first.  Both orders keep the longest blocks first, so no XCD ends with a
   // long block started late.
   int bh, qblock;
@@ -670,13 +670,13 @@ void attention32_kernel(AttnArgs a) {
     const int per_xcd = BH >> 3;
     const int slot = blockIdx.x >> 3;
     if (a.group > 0) {
-      // the XCDs walk the groups from the last rows down, eight neighbouring groups at a
-      // time: the projection that writes q, k and v finishes with the last rows, which are
-      // then still in the last-level cache (cfg5 forward 48.91 -> 48.78 ms on MI355X)
+      // each XCD walks its range's groups from the last down: the QKV projection walks the
+      // same eighths of the tokens upwards on the same XCDs, so the rows it wrote last are
+      // read first, while they are still in the XCD's L2 and the last-level cache
       const int G = a.group, per_grp = G * nqb;
       const int grp = slot / per_grp, r = slot - grp * per_grp;
       const int ngrp = per_xcd / G;
-      bh = ((ngrp - 1 - grp) * 8 + (blockIdx.x & 7)) * G + r % G;
+      bh = (blockIdx.x & 7) * per_xcd + (ngrp - 1 - grp) * G + r % G;
       qblock = nqb - 1 - r / G;
     } else {
       bh = (blockIdx.x & 7) * per_xcd + slot % per_xcd;

@@ -475,9 +475,19 @@ __global__ __launch_bounds__(kRT) void ffn_roles_kernel(FfnArgs a) {
   const int C = F / 32;
   const int64_t M = a.m;
   const int64_t ntiles = (M + kTok - 1) / kTok;
-  const int64_t tile0 = blockIdx.x;
-  if (tile0 >= ntiles) return;  // uniform per workgroup, before any barrier
-  const int my_tiles = (int)((ntiles - 1 - tile0) / gridDim.x) + 1;
+  // Tile order: XCD x (workgroup b runs on XCD b % 8) owns the x-th eighth of the tiles and
+  // walks it downwards.  The out-projection before it writes each eighth upwards on that XCD
+  // (its persistent tiles), and the projection after it reads each eighth upwards, so each
+  // kernel first reads what the one before wrote last, while it is still in the XCD's L2 and
+  // the last-level cache.
+  int64_t rs = 0, re = ntiles, slot = blockIdx.x, nsl = gridDim.x;
+  if ((gridDim.x & 7) == 0) {
+    const int x = blockIdx.x & 7;
+    rs = ntiles * x / 8; re = ntiles * (x + 1) / 8; slot = blockIdx.x >> 3; nsl = gridDim.x >> 3;
+  }
+  if (slot >= re - rs) return;  // uniform per workgroup, before any barrier
+  const int my_tiles = (int)((re - rs - 1 - slot) / nsl) + 1;
+  auto tile_of = [&](int64_t t) -> int64_t { return re - 1 - (slot + t * nsl); };
   const int G = my_tiles * C;   // steps with a stage-1 product; G + 2 steps in all
 
   const int l = threadIdx.x & 63, wave = wave_id();
@@ -547,7 +557,7 @@ __global__ __launch_bounds__(kRT) void ffn_roles_kernel(FfnArgs a) {
 
     issue(0, 0, 0, 0);      // W_in chunk 0 -> buffer 0 (W_out chunk 0 is copied again at step 0)
     issue(1 % C, 1, 0, 0);  // W_in chunk 1 -> buffer 1
-    load_x(tile0);
+    load_x(tile_of(0));
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
@@ -605,7 +615,7 @@ __global__ __launch_bounds__(kRT) void ffn_roles_kernel(FfnArgs a) {
             hout = mfma32x32(w, xf[i], hout);
           }
           if constexpr (LAST) {
-            if (tg + 1 < my_tiles) load_x(tile0 + (int64_t)(tg + 1) * gridDim.x);
+            if (tg + 1 < my_tiles) load_x(tile_of(tg + 1));
           }
           if constexpr (GELU) {
 #pragma unroll
@@ -789,7 +799,7 @@ __global__ __launch_bounds__(kRT) void ffn_roles_kernel(FfnArgs a) {
   for (int g = 2; g < G + 2; ++g) {
     s2(b3, g & 1);
     if (c2 >= C - 1 - PF_STEPS && c2 < C - 1) {
-      const int64_t r0 = (tile0 + t2 * gridDim.x) * kTok + 32 * sl + PF_ROWS * (c2 - (C - 1 - PF_STEPS));
+      const int64_t r0 = tile_of(t2) * kTok + 32 * sl + PF_ROWS * (c2 - (C - 1 - PF_STEPS));
 #pragma unroll
       for (int i = 0; i < PF_ROWS; ++i)
         if (r0 + i < M) dma16(pf_lane, a.residual + (r0 + i) * D, pf_sink);
@@ -798,7 +808,7 @@ __global__ __launch_bounds__(kRT) void ffn_roles_kernel(FfnArgs a) {
     // this W_out buffer
     __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
     lds_barrier();
-    if (c2 == C - 1) epilogue(tile0 + t2 * gridDim.x);
+    if (c2 == C - 1) epilogue(tile_of(t2));
     b3 = b3 == 2 ? 0 : b3 + 1;
     if (++c2 == C) { c2 = 0; ++t2; }
   }

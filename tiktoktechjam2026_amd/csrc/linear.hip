@@ -927,9 +927,19 @@ __global__ __launch_bounds__(64 * kXsWaves) void linear_xs_kernel(LinearArgs a) 
   const int N = a.n;
   const int NC = N / kXsRows;  // steps per tile (>= KS, checked by the launcher)
   const int64_t ntiles = (M + kXsTile - 1) / kXsTile;
-  const int64_t tile0 = blockIdx.x;
-  if (tile0 >= ntiles) return;  // uniform per workgroup, before any barrier
-  const int my_tiles = (int)((ntiles - 1 - tile0) / gridDim.x) + 1;
+  // Tile order: XCD x (workgroup b runs on XCD b % 8) owns the x-th eighth of the tiles and
+  // walks it upwards.  The fused FFN that writes this projection's input walks the same
+  // eighths downwards on the same XCDs, and the attention that reads its output walks them
+  // downwards again, so each kernel first reads what the one before wrote last, while it is
+  // still in the XCD's L2 and the last-level cache.
+  int64_t rs = 0, re = ntiles, slot = blockIdx.x, nsl = gridDim.x;
+  if ((gridDim.x & 7) == 0) {
+    const int x = blockIdx.x & 7;
+    rs = ntiles * x / 8; re = ntiles * (x + 1) / 8; slot = blockIdx.x >> 3; nsl = gridDim.x >> 3;
+  }
+  if (slot >= re - rs) return;  // uniform per workgroup, before any barrier
+  const int my_tiles = (int)((re - rs - 1 - slot) / nsl) + 1;
+  auto tile_of = [&](int64_t t) { return rs + slot + t * nsl; };
 
   const int l = threadIdx.x & 63, wave = wave_id();
   const int r = l & 15, g = l >> 4;
@@ -963,7 +973,7 @@ __global__ __launch_bounds__(64 * kXsWaves) void linear_xs_kernel(LinearArgs a) 
   // ---- X fragments: [t][ks] = token 16 t + r of the wave's 32, k = 32 ks + 8 g .. + 7 ----
   const uint32_t xoff = (uint32_t)(r * K + 8 * g) * 2u;
   auto x_rsrc = [&](int tile_i) {
-    const int64_t row0 = (tile0 + (int64_t)tile_i * gridDim.x) * kXsTile + 32 * wave;
+    const int64_t row0 = tile_of(tile_i) * kXsTile + 32 * wave;
     const uint32_t rows = (uint32_t)max<int64_t>(0, min<int64_t>(32, M - row0));
     return make_rsrc(X + row0 * K, rows * (uint32_t)(K * 2));
   };
@@ -1075,7 +1085,7 @@ __global__ __launch_bounds__(64 * kXsWaves) void linear_xs_kernel(LinearArgs a) 
   // loaded X only when NC == KS.
   auto run_tile = [&](int tile_i, h8 (&xc)[2][KS], h8 (&xn)[2][KS]) {
     const bool has_next = tile_i + 1 < my_tiles;
-    const int64_t row0 = (tile0 + (int64_t)tile_i * gridDim.x) * kXsTile + 32 * wave;
+    const int64_t row0 = tile_of(tile_i) * kXsTile + 32 * wave;
     const uint32_t rows = (uint32_t)max<int64_t>(0, min<int64_t>(32, M - row0));
     const __amdgpu_buffer_rsrc_t yr = make_rsrc(Y + row0 * N, rows * (uint32_t)N * (uint32_t)sizeof(OT));
     const __amdgpu_buffer_rsrc_t xr = has_next ? x_rsrc(tile_i + 1) : make_rsrc(X, 0u);
