@@ -165,7 +165,9 @@ int mpk_attention_auto_variant(int32_t batch, int32_t heads, int32_t seq_len, in
 /*
  * mpk_causal_attention for FP16 q / k / v whose q already holds q * scale * log2(e), rounded to
  * FP16 once by its producer (mpk_linear_qscaled): the 32x32 kernel (head_dim 32 or 64, variant 0
- * or 6-8; variant 0 picks 6 at head_dim 32) with the scores already in log2 units, so no
+ * or 6-8; variant 0 picks, at head_dim 32, 7 where its launch is large enough for the grouped
+ * schedule - B*H a multiple of 64 and (B*H / 8) * ceil(S / 256) >= 1024 - and 6 otherwise) with
+ * the scores already in log2 units, so no
  * per-score scaling.  out_dtype kF16 or kF32.
  * Replaces, with the scale moved into the projection: fp16_causal_attention
  * (custom_kernel/triton_attention.py:341-390).

@@ -1354,11 +1354,17 @@ extern "C" int mpk_causal_attention_prescaled(const void* q, const void* k, cons
   if (batch < 0 || heads <= 0 || seq_len < 0) return MPK_EINVAL;
   if (out_dtype != kF32 && out_dtype != kF16) return MPK_EINVAL;
   if (head_dim != 32 && head_dim != 64) return MPK_EUNSUPPORTED;
-  // built-in choice: 4-wave workgroups at head dim 32 (without the per-score FMA they are at
-  // least as fast as the 8-wave ones at every length measured on MI355X: 764 vs 783 us alone
-  // at B64 H8 S4096, level within 0.2 % in the whole cfg5 forward), as
-  // mpk_attention_auto_variant at head dim 64
-  if (variant == 0) variant = head_dim == 32 ? 6 : (seq_len < 1024 ? 7 : 6);
+  // built-in choice at head dim 32: 8-wave workgroups where their launch runs the grouped
+  // schedule (many rounds of workgroups: cfg5's B64 H8 S4096 per microbatch), where the whole
+  // cfg5 forward measured 47.50-47.58 ms against 48.18-48.28 ms with 4-wave workgroups in one
+  // process on MI355X (the kernel alone had been 783 vs 764 us before the layer chain's tile
+  // order; cfg2's S1024 is level); 4-wave workgroups otherwise.  Head dim 64 as
+  // mpk_attention_auto_variant.
+  if (variant == 0) {
+    const int64_t rows = (int64_t)batch * heads, nqb8 = ((int64_t)seq_len + 255) / 256;
+    const bool grouped8 = rows % 64 == 0 && (rows / 8) * nqb8 >= 1024;
+    variant = head_dim == 32 ? (grouped8 ? 7 : 6) : (seq_len < 1024 ? 7 : 6);
+  }
   if (variant < 6 || variant > 8) return MPK_EUNSUPPORTED;
   const int64_t* st[4] = {q_strides, k_strides, v_strides, o_strides};
   const void* base[4] = {q, k, v, o};
