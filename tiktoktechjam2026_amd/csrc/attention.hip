@@ -641,7 +641,7 @@ void attention32_kernel(AttnArgs a) {
   static_assert(HD == 32 || HD == 64, "head dim");
   static_assert(KTILE % 32 == 0 && KTILE <= NT, "key tile");
 
-  __shared__ _Float16 ks_lds[2][SH::KBUF];
+  __shared__ __align__(16) _Float16 ks_lds[2][SH::KBUF];
   // V is staged row-major like K (one 16-byte store per chunk); the P V product
   // reads its V^T fragments with LDS transpose loads (ds_read_b64_tr_b16).  Each
   // 32-lane half of such a read covers 4 consecutive keys x 64 bytes of head dims,
@@ -651,7 +651,7 @@ void attention32_kernel(AttnArgs a) {
   // unpadded rows at hd 32.  (At hd 64 that takes 192-byte rows, which measured no
   // faster than the K stride; hd 64 keeps it.)
   constexpr int LDVR = HD == 32 ? HD : SH::LDK;
-  __shared__ _Float16 vr_lds[2][KTILE * LDVR];
+  __shared__ __align__(16) _Float16 vr_lds[2][KTILE * LDVR];
   __shared__ float kbias[2][KTILE];
 
   const int S = a.seq;
@@ -817,6 +817,40 @@ void attention32_kernel(AttnArgs a) {
   bool bias_staged = false;
   const uint32_t krow_bytes = (uint32_t)(a.ks[2] * (int64_t)sizeof(IT));
   const uint32_t vrow_bytes = (uint32_t)(a.vs[2] * (int64_t)sizeof(IT));
+  // FP16 inputs at head dim 32: K and V tiles travel global -> LDS as LDS-DMA copies (1 KB
+  // each, no registers; K rows padded to LDK halves, the pad units filled from the row's
+  // start; keys past the sequence copy its last row, which the key bias masks), issued
+  // round-robin by the waves at the start of a step and awaited (vmcnt 0: the loop issues no
+  // other vector-memory operation) before its barrier.  Measured on MI355X in one process,
+  // outputs bit-identical: cfg5 forward 48.61-48.63 vs 49.03-49.06 ms, cfg2 level; at head
+  // dim 64 (cfg4) the register staging below stays, 2.594 vs 2.603 ms.
+  constexpr bool DMA_KV = !F32IN && HD == 32;
+  constexpr int KUP = SH::LDK / 8, VUP = LDVR / 8, KU = HD / 8;
+  constexpr int KCOPIES = KTILE * KUP / 64, VCOPIES = KTILE * VUP / 64;
+  static_assert(!DMA_KV || (KTILE * KUP % 64 == 0 && KTILE * VUP % 64 == 0), "whole copies");
+  auto fetch_dma = [&](int kb, int buf) {
+    const int last = S - 1 - kb;  // last key of the sequence, relative to the tile
+    const uint32_t kl = (uint32_t)(uintptr_t)(lds_void*)ks_lds[buf];
+    const uint32_t vl = (uint32_t)(uintptr_t)(lds_void*)vr_lds[buf];
+    const _Float16* kbase = reinterpret_cast<const _Float16*>(Kp) + (int64_t)kb * a.ks[2];
+    const _Float16* vbase = reinterpret_cast<const _Float16*>(Vp) + (int64_t)kb * a.vs[2];
+    for (int j = wave; j < KCOPIES + VCOPIES; j += NW) {
+      if (j < KCOPIES) {
+        const int u = 64 * j + l, key = min(u / KUP, last), pos = u % KUP;
+        dma16((uint32_t)key * krow_bytes + (pos < KU ? 16u * pos : 0u), kbase, (uint32_t)__builtin_amdgcn_readfirstlane((int)(kl + 1024u * j)));
+      } else {
+        const int u = 64 * (j - KCOPIES) + l, key = min(u / VUP, last), pos = u % VUP;
+        dma16((uint32_t)key * vrow_bytes + (pos < KU ? 16u * pos : 0u), vbase, (uint32_t)__builtin_amdgcn_readfirstlane((int)(vl + 1024u * (j - KCOPIES))));
+      }
+    }
+    bias_staged = KEYMASK || kb + KTILE > S;
+    if (bias_staged && threadIdx.x < KTILE) {
+      const int gk = kb + threadIdx.x;
+      bool valid = gk < S;
+      if (KEYMASK && valid) valid = kv_valid[gk] != 0;
+      kbias[buf][threadIdx.x] = valid ? 0.f : -INFINITY;
+    }
+  };
   auto fetch = [&](int kb) {
     const uint32_t rows = (uint32_t)min(KTILE, S - kb);
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(Kp + (int64_t)kb * a.ks[2], rows * krow_bytes);
@@ -1134,8 +1168,9 @@ void attention32_kernel(AttnArgs a) {
     }
   };
 
-  // One step per key tile: prefetch the next tile into registers, process this
-  // one, stage the next into the other LDS buffer, one barrier.  Tiles below the
+  // One step per key tile: prefetch the next tile into registers (or copy it into the other
+  // LDS buffer by LDS-DMA), process this one, stage the next into the other LDS buffer, one
+  // barrier.  Tiles below the
   // workgroup's first query (and inside the sequence) are visible to every query
   // of every wave and run the check-free steady-state body in a loop of their
   // own; the split point is workgroup-uniform, so every wave meets the same
@@ -1146,16 +1181,29 @@ void attention32_kernel(AttnArgs a) {
   auto step_in = [&](int tile, int cur, auto first_tag, auto edge_tag) {
     const int kb = tile * KTILE;
     const bool more = tile + 1 < ntiles;
-    if (more) fetch(kb + KTILE);
+    if constexpr (DMA_KV) {
+      if (more) fetch_dma(kb + KTILE, cur ^ 1);
+    } else {
+      if (more) fetch(kb + KTILE);
+    }
     process(kb, ks_lds[cur], vr_lds[cur], kbias[cur], first_tag, edge_tag);
-    if (more) stash(cur ^ 1);
+    if constexpr (DMA_KV) {
+      wait_copies<0>();
+    } else {
+      if (more) stash(cur ^ 1);
+    }
     __syncthreads();
   };
   auto step = [&](int tile, auto first_tag, auto edge_tag) { step_in(tile, tile & 1, first_tag, edge_tag); };
   const int steady_end = KEYMASK ? 1 : max(1, min(ntiles, (a.causal ? min(q0, S) : S) / KTILE));
 
-  fetch(0);
-  stash(0);
+  if constexpr (DMA_KV) {
+    fetch_dma(0, 0);
+    wait_copies<0>();
+  } else {
+    fetch(0);
+    stash(0);
+  }
   __syncthreads();
   step(0, std::true_type{}, std::true_type{});
   int tile = 1;
